@@ -1,0 +1,184 @@
+/*
+ * jangq_amd — C ABI of the MI355X (gfx950) quantized-weight matmul path.
+ *
+ * Storage contract (JANG v2 / MLX affine, reference FORMAT.md:57-90, format/spec.py:6-30):
+ *   codes   uint32 [rows, K*bits/32]   LSB-first bitstream of `bits`-bit codes along K
+ *                                      (jang-tools/jang_tools/pack.py:12-149); 3/5/6-bit
+ *                                      codes straddle word boundaries.
+ *   scales  [rows, K/group_size]       bf16, f16 or f32 (JQ_BF16 / JQ_F16 / JQ_F32)
+ *   biases  [rows, K/group_size]       same dtype as scales
+ *   w[r,k] = fl(fl(q[r,k] * scale[r,k/gs]) + bias[r,k/gs])   in fp32
+ *                                      (jang-tools/jang_tools/affine.py:445-463)
+ *   bits in {2,3,4,5,6,8}, group_size in {32,64,128}, K % group_size == 0.
+ *   3-D expert stacks are [E, rows, ...] and contiguous.
+ *
+ * Conventions
+ *   - Every pointer argument is caller-owned device memory (except where noted as host).
+ *     No entry point allocates device memory, synchronises the stream or keeps state
+ *     between calls, except the documented workspace arguments.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL is the default stream).
+ *   - Return value: JQ_OK (0) or a negative JQ_ERR_* code. Nothing throws across the ABI.
+ *     Shapes, bits, group sizes and dtypes are validated on the host before any launch.
+ */
+#ifndef JANGQ_AMD_H
+#define JANGQ_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* jq_stream_t; /* == hipStream_t */
+
+#define JQ_ABI_VERSION 1
+
+enum jq_status {
+  JQ_OK = 0,
+  JQ_ERR_BITS = -1,        /* bits not in {2,3,4,5,6,8} */
+  JQ_ERR_GROUP_SIZE = -2,  /* group_size not in {32,64,128} or K % group_size != 0 */
+  JQ_ERR_SHAPE = -3,       /* a dimension is negative, too large or inconsistent */
+  JQ_ERR_DTYPE = -4,       /* unsupported dtype code for this argument */
+  JQ_ERR_NULL = -5,        /* a required pointer is NULL while its extent is non-zero */
+  JQ_ERR_LAUNCH = -6,      /* the HIP runtime reported an error at launch */
+  JQ_ERR_WORKSPACE = -7,   /* workspace missing or smaller than the size query returned */
+  JQ_ERR_INDEX = -8,       /* an index argument is out of range (checked where cheap) */
+};
+
+enum jq_dtype {
+  JQ_F32 = 0,
+  JQ_BF16 = 1,
+  JQ_F16 = 2,
+};
+
+/* ABI version of the loaded library (JQ_ABI_VERSION at build time). */
+int jq_abi_version(void);
+
+/* Static string for a status code. */
+const char* jq_status_string(int status);
+
+/*
+ * Unpack codes to one uint8 per element: out[r, k] = q[r, k].
+ * Replaces jang-tools/jang_tools/pack.py:85-149 (unpack_bits) applied to a packed uint32
+ * matrix viewed as bytes (affine.py:457).
+ */
+int jq_unpack(const uint32_t* codes, int bits, int64_t rows, int64_t K,
+              uint8_t* out, jq_stream_t stream);
+
+/*
+ * Dequantize: out[r, k] = fl(fl(q*s) + b) in fp32, stored as out_dtype (bf16/f16 are the
+ * round-to-nearest-even of that fp32 value). Bit-exact with the fp32 reference.
+ * Replaces jang-tools/jang_tools/affine.py:445-463 (dequantize_affine_numpy) and the
+ * mx.dequantize call at jang-tools/jang_tools/loader.py:469.
+ */
+int jq_dequantize(const uint32_t* codes, const void* scales, const void* biases,
+                  int sb_dtype, int bits, int group_size, int64_t rows, int64_t K,
+                  void* out, int out_dtype, jq_stream_t stream);
+
+/*
+ * Affine group quantization with MLX's rule (dominant edge, signed scale, eps 1e-7,
+ * round-half-even), codes packed LSB-first. w_dtype is the source dtype (converted to fp32
+ * exactly). sb_dtype: JQ_BF16 (MLX runtime sidecars), JQ_F16 (converter sidecars, with the
+ * non-zero f16 scale guard) or JQ_F32.
+ * Replaces jang-tools/jang_tools/affine.py:193-276 (quantize_native_affine_numpy, the CPU
+ * mirror of mx.quantize) as called from jang-tools/jang_tools/convert.py:602-645.
+ */
+int jq_quantize(const void* w, int w_dtype, int bits, int group_size, int64_t rows,
+                int64_t K, uint32_t* codes, void* scales, void* biases, int sb_dtype,
+                jq_stream_t stream);
+
+/*
+ * y[M, N] = x[M, K] @ dequant(W)[N, K]^T  (transpose=True), fp32 accumulation.
+ * x_dtype: JQ_BF16 / JQ_F16 / JQ_F32; y_dtype likewise (MLX returns x.dtype).
+ * Replaces mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits) as
+ * called from jang-tools/jang_tools/jangrt/linear.py:41-45 and
+ * jang-tools/jang_tools/dots3/ops.py:44-51. Small M runs the decode GEMV kernels, larger
+ * M the matrix-core GEMM.
+ */
+int jq_quantized_matmul(const void* x, int x_dtype, const uint32_t* codes,
+                        const void* scales, const void* biases, int sb_dtype, int bits,
+                        int group_size, int64_t M, int64_t N, int64_t K, void* y,
+                        int y_dtype, jq_stream_t stream);
+
+/*
+ * Grouped form of jq_quantized_matmul: `count` independent problems sharing x_dtype,
+ * y_dtype and sb_dtype, in ONE launch when they share M, K, bits and group_size (q/k/v or
+ * gate/up projections of one token batch). Each array has `count` entries.
+ * No reference counterpart as one call: it replaces `count` consecutive
+ * mx.quantized_matmul calls on the same x (jang-tools/jang_tools/dots3/ops.py:79-93).
+ */
+int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
+                              const uint32_t* const* codes, const void* const* scales,
+                              const void* const* biases, int sb_dtype, const int* bits,
+                              const int* group_size, const int64_t* M, const int64_t* N,
+                              const int64_t* K, void* const* y, int y_dtype,
+                              jq_stream_t stream);
+
+/*
+ * Router: probs = softmax(logits) in fp32 (max-subtracted, "precise"), top-k expert ids
+ * per token (ties -> lower id first), weights = their probabilities, optionally divided
+ * by their sum (norm_topk_prob). logits f32 [T, E]; idx uint32 [T, k]; weights f32 [T, k].
+ * Ids are written in descending-probability order.
+ * Replaces the caller-side routing of jang-tools/jang_tools/qwen4_exp/modeling.py:587-593
+ * (softmax(precise=True) -> argpartition -> take_along_axis -> renorm).
+ */
+int jq_moe_route(const float* logits, int64_t T, int64_t E, int k, int renorm,
+                 uint32_t* idx, float* weights, jq_stream_t stream);
+
+/*
+ * Workspace bytes needed by jq_gather_qmm for n_pairs (token, expert) pairs over E experts
+ * with M activation rows per pair (jq_switch_glu: M = 1, n_pairs = T*k). Host-only.
+ * Returns -1 for invalid arguments.
+ */
+int64_t jq_gather_workspace_size(int64_t n_pairs, int64_t E, int64_t M);
+
+/*
+ * out[i] = x[lhs[i]] @ dequant(W[rhs[i]])^T for i < n_pairs.
+ *   x     [x_batch, M, K]   (x_dtype)
+ *   W     codes [E, N, K*bits/32], scales/biases [E, N, K/gs]
+ *   lhs   uint32 [n_pairs] (NULL means lhs[i] = i, x_batch must be >= n_pairs)
+ *   rhs   uint32 [n_pairs] expert ids (< E)
+ *   out   [n_pairs, M, N]  (y_dtype)
+ * Pairs are grouped by expert on the device so each selected expert's packed weights are
+ * streamed once per call whatever the order of rhs; `sorted_indices` is accepted for
+ * signature parity and changes nothing (the device grouping is always exact). Pairs whose
+ * expert id is >= E are skipped (their output rows are not written).
+ * Replaces mx.gather_qmm(x, w, scales, biases, lhs_indices, rhs_indices, transpose=True,
+ * group_size, bits, sorted_indices) as called from jang-tools/jang_tools/dsv41/model.py:855-857
+ * and jang-tools/jang_tools/dots3/ops.py:168-192.
+ */
+int jq_gather_qmm(const void* x, int x_dtype, int64_t x_batch, int64_t M,
+                  const uint32_t* codes, const void* scales, const void* biases,
+                  int sb_dtype, int bits, int group_size, int64_t E, int64_t N, int64_t K,
+                  const uint32_t* lhs, const uint32_t* rhs, int64_t n_pairs,
+                  int sorted_indices, void* out, int y_dtype, void* workspace,
+                  int64_t workspace_bytes, jq_stream_t stream);
+
+/*
+ * SwitchGLU over stacked experts: for every (token t, slot j) pair with e = idx[t, j]:
+ *   h = silu(x[t] @ Wg[e]^T) * (x[t] @ Wu[e]^T)     (each projection rounded to y_dtype
+ *                                                    first, as three gather_qmm calls do)
+ *   out[t, j] = h @ Wd[e]^T
+ * x [T, H] (x_dtype); idx uint32 [T, k]; out [T, k, H] (y_dtype).
+ * gate/up codes [E, I, H*bits_gu/32], scales/biases [E, I, H/gs];
+ * down codes [E, H, I*bits_d/32], scales/biases [E, H, I/gs].
+ * h_buf: caller scratch of T*k*I elements of y_dtype (the SwiGLU activations).
+ * One grouped launch computes gate+up+SwiGLU for all active experts, a second the down
+ * projection. Replaces mlx_lm SwitchGLU.__call__ as restated at
+ * jang-tools/jang_tools/dots3/ops.py:195-223 and jang-tools/jang_tools/jangrt/switchglu_decode.py:161-183
+ * (both the sorted and unsorted branches compute the same values).
+ */
+int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E,
+                  const uint32_t* idx, int k,
+                  const uint32_t* gate_codes, const void* gate_scales, const void* gate_biases,
+                  const uint32_t* up_codes, const void* up_scales, const void* up_biases,
+                  int bits_gu,
+                  const uint32_t* down_codes, const void* down_scales, const void* down_biases,
+                  int bits_d, int sb_dtype, int group_size, void* h_buf, void* out,
+                  int y_dtype, void* workspace, int64_t workspace_bytes, jq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JANGQ_AMD_H */

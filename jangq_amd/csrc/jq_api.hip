@@ -1,0 +1,123 @@
+// Dense matmul entry points: dispatch between the decode GEMV (M <= 4, or any shape the
+// matrix-core kernel does not take) and the matrix-core GEMM.
+#include "jq_common.h"
+#include "jq_qmv.h"
+
+namespace {
+
+int dense_one(const void* x, int xd, const uint32_t* codes, const void* scales,
+              const void* biases, int sb, int bits, int gs, int64_t M, int64_t N, int64_t K,
+              void* y, int yd, hipStream_t st) {
+  const bool mfma_ok = (xd == JQ_BF16 || xd == JQ_F16) && K % 128 == 0;
+  if (M > 4 && mfma_ok) {
+    jqk::QmmProblem p;
+    p.x = x; p.codes = codes; p.scales = scales; p.biases = biases; p.y = y;
+    p.M = M; p.N = N; p.K = K;
+    p.expert_stride_codes = 0;
+    p.expert_stride_sb = 0;
+    return jqk::qmm_launch(p, bits, gs, xd, sb, yd, st);
+  }
+  // GEMV in slices of at most 4 token rows.
+  const int xs = jqh::dtype_size(xd), ys = jqh::dtype_size(yd);
+  for (int64_t m0 = 0; m0 < M; m0 += 4) {
+    jqk::QmvBatch b;
+    b.M = (int)(M - m0 < 4 ? M - m0 : 4);
+    b.K = (int)K;
+    b.p[0].x = (const char*)x + m0 * K * xs;
+    b.p[0].codes = codes;
+    b.p[0].scales = scales;
+    b.p[0].biases = biases;
+    b.p[0].N = N;
+    b.p[0].y = (char*)y + m0 * N * ys;
+    const int s = jqk::qmv_launch(b, 1, bits, gs, xd, sb, yd, st);
+    if (s) return s;
+  }
+  return JQ_OK;
+}
+
+int check_dense(const void* x, int xd, const uint32_t* codes, const void* scales,
+                const void* biases, int sb, int bits, int gs, int64_t M, int64_t N, int64_t K,
+                void* y, int yd) {
+  int s = jqh::check_qshape(bits, gs, N, K);
+  if (s) return s;
+  if (M < 0 || M > ((int64_t)1 << 31)) return JQ_ERR_SHAPE;
+  if (!jqh::dtype_ok(xd) || !jqh::dtype_ok(sb) || !jqh::dtype_ok(yd)) return JQ_ERR_DTYPE;
+  if (M > 0 && N > 0 && K > 0 && (!x || !codes || !scales || !biases || !y)) return JQ_ERR_NULL;
+  if (M > 0 && N > 0 && K == 0 && !y) return JQ_ERR_NULL;
+  return JQ_OK;
+}
+
+__global__ void fill_zero_kernel(void* y, int64_t n, int es) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    if (es == 4) ((float*)y)[i] = 0.f;
+    else ((uint16_t*)y)[i] = 0;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int jq_quantized_matmul(const void* x, int x_dtype, const uint32_t* codes, const void* scales,
+                        const void* biases, int sb_dtype, int bits, int group_size, int64_t M,
+                        int64_t N, int64_t K, void* y, int y_dtype, jq_stream_t stream) {
+  int s = check_dense(x, x_dtype, codes, scales, biases, sb_dtype, bits, group_size, M, N, K, y,
+                      y_dtype);
+  if (s) return s;
+  if (M == 0 || N == 0) return JQ_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (K == 0) {  // empty contraction: y = 0
+    const int64_t n = M * N;
+    fill_zero_kernel<<<(unsigned)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536), 256, 0, st>>>(
+        y, n, jqh::dtype_size(y_dtype));
+    return jqh::launch_status();
+  }
+  return dense_one(x, x_dtype, codes, scales, biases, sb_dtype, bits, group_size, M, N, K, y,
+                   y_dtype, st);
+}
+
+int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
+                              const uint32_t* const* codes, const void* const* scales,
+                              const void* const* biases, int sb_dtype, const int* bits,
+                              const int* group_size, const int64_t* M, const int64_t* N,
+                              const int64_t* K, void* const* y, int y_dtype, jq_stream_t stream) {
+  if (count < 0) return JQ_ERR_SHAPE;
+  if (count == 0) return JQ_OK;
+  if (!x || !codes || !scales || !biases || !bits || !group_size || !M || !N || !K || !y)
+    return JQ_ERR_NULL;
+  for (int i = 0; i < count; ++i) {
+    int s = check_dense(x[i], x_dtype, codes[i], scales[i], biases[i], sb_dtype, bits[i],
+                        group_size[i], M[i], N[i], K[i], y[i], y_dtype);
+    if (s) return s;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  bool same = count <= jqk::kMaxProblems;
+  for (int i = 1; i < count && same; ++i)
+    same = bits[i] == bits[0] && group_size[i] == group_size[0] && M[i] == M[0] && K[i] == K[0];
+  if (same && M[0] >= 1 && M[0] <= 4 && K[0] > 0) {
+    jqk::QmvBatch b;
+    b.M = (int)M[0];
+    b.K = (int)K[0];
+    int n = 0;
+    for (int i = 0; i < count; ++i) {
+      if (N[i] == 0) continue;
+      b.p[n].x = x[i];
+      b.p[n].codes = codes[i];
+      b.p[n].scales = scales[i];
+      b.p[n].biases = biases[i];
+      b.p[n].y = y[i];
+      b.p[n].N = N[i];
+      ++n;
+    }
+    return jqk::qmv_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
+  }
+  for (int i = 0; i < count; ++i) {
+    int s = jq_quantized_matmul(x[i], x_dtype, codes[i], scales[i], biases[i], sb_dtype, bits[i],
+                                group_size[i], M[i], N[i], K[i], y[i], y_dtype, stream);
+    if (s) return s;
+  }
+  return JQ_OK;
+}
+
+}  // extern "C"

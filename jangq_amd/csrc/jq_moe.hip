@@ -1,0 +1,308 @@
+// MoE path: router top-k, device-side grouping of (token, expert) pairs by expert, and the
+// grouped gather_qmm / SwitchGLU launches.
+//
+// Caller side restated from the reference:
+//   routing  softmax(logits, precise) -> top-k -> gather -> renorm
+//            (jang-tools/jang_tools/qwen4_exp/modeling.py:587-593)
+//   grouping mlx_lm _gather_sort / _scatter_unsort around gather_qmm(sorted_indices=True)
+//            (jang-tools/jang_tools/dots3/ops.py:202-214, jangrt/switchglu_decode.py:161-183)
+// Here the grouping never leaves the device and never changes values: every pair's output
+// row is computed from its own activations and its expert's weights, whatever the order.
+#include "jq_common.h"
+#include "jq_qmv.h"
+
+namespace {
+
+using namespace jq;
+
+// Rows per tile of the grouped matrix-core kernel (must match qmm_gather_launch).
+constexpr int kTileRows = 16;
+constexpr int kMaxExperts = 4096;
+
+// One wave per token. Lanes hold E/64 logits each; top-k by k rounds of wave argmax
+// (ties -> lowest expert id), probabilities from a max-subtracted fp32 softmax.
+__global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ logits, int T, int E,
+                                                    int k, int renorm, uint32_t* __restrict__ idx,
+                                                    float* __restrict__ wout) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float* row = logits + (int64_t)t * E;
+  float mx = -INFINITY;
+  for (int e = lane; e < E; e += 64) mx = fmaxf(mx, row[e]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  float sum = 0.f;
+  for (int e = lane; e < E; e += 64) sum += expf(row[e] - mx);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  const float inv = 1.0f / sum;
+
+  // Selection runs on the logits (softmax is monotone); chosen ones are masked by id.
+  uint64_t chosen = 0;  // per-lane bitmask over its slots (E <= 4096 -> <= 64 slots)
+  float wsum = 0.f, wsel = 0.f;
+  int my_id = 0;
+  for (int j = 0; j < k; ++j) {
+    float best = -INFINITY;
+    int bid = 0x7FFFFFFF;
+    int slot = 0;
+    for (int e = lane; e < E; e += 64, ++slot) {
+      if ((chosen >> slot) & 1ull) continue;
+      const float v = row[e];
+      if (v > best || (v == best && e < bid)) { best = v; bid = e; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(best, o, 64);
+      const int oid = __shfl_xor(bid, o, 64);
+      if (ov > best || (ov == best && oid < bid)) { best = ov; bid = oid; }
+    }
+    if ((bid & 63) == lane) chosen |= 1ull << (bid >> 6);
+    const float p = expf(best - mx) * inv;
+    wsum += p;
+    if (lane == j) { wsel = p; my_id = bid; }
+  }
+  if (lane < k) {
+    idx[(int64_t)t * k + lane] = (uint32_t)my_id;
+    wout[(int64_t)t * k + lane] = renorm ? wsel / wsum : wsel;
+  }
+}
+
+JQ_DEV int block_exclusive_scan(int v, int* sh_wave, int& total) {
+  // 1024 threads = 16 waves.
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int n = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += n;
+  }
+  if (lane == 63) sh_wave[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < 16 ? sh_wave[lane] : 0;
+    int wi = w;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const int n = __shfl_up(wi, o, 64);
+      if (lane >= o) wi += n;
+    }
+    if (lane < 16) sh_wave[16 + lane] = wi - w;  // exclusive wave offsets
+    if (lane == 15) sh_wave[32] = wi;
+  }
+  __syncthreads();
+  total = sh_wave[32];
+  const int r = sh_wave[16 + wave] + incl - v;
+  __syncthreads();
+  return r;
+}
+
+// Single block of 1024 threads. Builds, for the pair list rhs[n_pairs] over E experts:
+//   seg_off[E+1]  exclusive offsets of each expert's segment in `order`
+//   order         pair ids grouped by expert (order inside a segment is arbitrary: it does
+//                 not change any value). Pairs whose expert id is >= E are left out.
+//   tiles         (expert, first row, rows) for every kTileRows-row tile of every segment
+//                 (segment rows = count * M)
+//   n_tiles[0]    number of tiles
+__global__ void __launch_bounds__(1024) plan_kernel(const uint32_t* __restrict__ rhs, int n_pairs,
+                                                    int E, int M, int* seg_off, uint32_t* order,
+                                                    int4* tiles, int* n_tiles) {
+  __shared__ int cnt[kMaxExperts];
+  __shared__ int cur[kMaxExperts];
+  __shared__ int sh_wave[40];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < n_pairs; i += 1024) {
+    const uint32_t e = rhs[i];
+    if (e < (uint32_t)E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  // Each thread owns a contiguous run of ceil(E/1024) experts.
+  const int per = (E + 1023) / 1024;
+  const int e0 = tid * per;
+  int local = 0, ltiles = 0;
+  for (int e = e0; e < e0 + per && e < E; ++e) {
+    local += cnt[e];
+    ltiles += (cnt[e] * M + kTileRows - 1) / kTileRows;
+  }
+  int total;
+  int base = block_exclusive_scan(local, sh_wave, total);
+  int ttotal;
+  int tbase = block_exclusive_scan(ltiles, sh_wave, ttotal);
+  for (int e = e0; e < e0 + per && e < E; ++e) {
+    seg_off[e] = base;
+    cur[e] = base;
+    const int rows = cnt[e] * M;
+    for (int r = 0; r < rows; r += kTileRows) {
+      tiles[tbase++] = make_int4(e, r, rows - r < kTileRows ? rows - r : kTileRows, 0);
+    }
+    base += cnt[e];
+  }
+  if (tid == 0) {
+    seg_off[E] = total;
+    *n_tiles = ttotal;
+  }
+  __syncthreads();
+  for (int i = tid; i < n_pairs; i += 1024) {
+    const uint32_t e = rhs[i];
+    if (e < (uint32_t)E) order[atomicAdd(&cur[e], 1)] = (uint32_t)i;
+  }
+}
+
+struct WsLayout {
+  int64_t seg_off, order, tiles, n_tiles, total;
+};
+
+inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+inline int64_t max_tiles_for(int64_t n_pairs, int64_t E, int64_t M) {
+  const int64_t active = n_pairs < E ? n_pairs : E;
+  return (n_pairs * M + kTileRows - 1) / kTileRows + active;
+}
+
+inline WsLayout ws_layout(int64_t n_pairs, int64_t E, int64_t M) {
+  WsLayout L;
+  int64_t o = 0;
+  L.seg_off = o; o = align256(o + (E + 1) * 4);
+  L.order = o; o = align256(o + n_pairs * 4);
+  L.tiles = o; o = align256(o + max_tiles_for(n_pairs, E, M) * 16);
+  L.n_tiles = o; o = align256(o + 4);
+  L.total = o;
+  return L;
+}
+
+int build_plan(const uint32_t* rhs, int64_t n_pairs, int64_t E, int64_t M, void* ws,
+               jqk::GatherPlan& plan, const uint32_t* lhs, hipStream_t st) {
+  const WsLayout L = ws_layout(n_pairs, E, M);
+  char* base = (char*)ws;
+  plan.seg_off = (const int*)(base + L.seg_off);
+  plan.order = (const uint32_t*)(base + L.order);
+  plan.tiles = (const int4*)(base + L.tiles);
+  plan.n_tiles = (const int*)(base + L.n_tiles);
+  plan.lhs = lhs;
+  plan.M = (int)M;
+  plan.pair_div = 1;
+  plan.x_rows = 0;
+  plan_kernel<<<1, 1024, 0, st>>>(rhs, (int)n_pairs, (int)E, (int)M, (int*)(base + L.seg_off),
+                                  (uint32_t*)(base + L.order), (int4*)(base + L.tiles),
+                                  (int*)(base + L.n_tiles));
+  return jqh::launch_status();
+}
+
+int check_expert_shape(int bits, int gs, int64_t E, int64_t N, int64_t K) {
+  int s = jqh::check_qshape(bits, gs, N, K);
+  if (s) return s;
+  if (E <= 0 || E > kMaxExperts) return JQ_ERR_SHAPE;
+  return JQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int jq_moe_route(const float* logits, int64_t T, int64_t E, int k, int renorm, uint32_t* idx,
+                 float* weights, jq_stream_t stream) {
+  if (T < 0 || E <= 0 || E > kMaxExperts || k <= 0 || k > E || k > 64) return JQ_ERR_SHAPE;
+  if (T == 0) return JQ_OK;
+  if (!logits || !idx || !weights) return JQ_ERR_NULL;
+  route_kernel<<<(unsigned)((T + 3) / 4), 256, 0, (hipStream_t)stream>>>(
+      logits, (int)T, (int)E, k, renorm, idx, weights);
+  return jqh::launch_status();
+}
+
+int64_t jq_gather_workspace_size(int64_t n_pairs, int64_t E, int64_t M) {
+  if (n_pairs < 0 || E <= 0 || M <= 0) return -1;
+  return ws_layout(n_pairs, E, M).total;
+}
+
+int jq_gather_qmm(const void* x, int x_dtype, int64_t x_batch, int64_t M, const uint32_t* codes,
+                  const void* scales, const void* biases, int sb_dtype, int bits, int group_size,
+                  int64_t E, int64_t N, int64_t K, const uint32_t* lhs, const uint32_t* rhs,
+                  int64_t n_pairs, int sorted_indices, void* out, int y_dtype, void* workspace,
+                  int64_t workspace_bytes, jq_stream_t stream) {
+  int s = check_expert_shape(bits, group_size, E, N, K);
+  if (s) return s;
+  if (x_dtype != JQ_BF16 && x_dtype != JQ_F16) return JQ_ERR_DTYPE;
+  if (!jqh::dtype_ok(sb_dtype) || !jqh::dtype_ok(y_dtype)) return JQ_ERR_DTYPE;
+  if (M <= 0 || x_batch < 0 || n_pairs < 0) return JQ_ERR_SHAPE;
+  if (K % 128) return JQ_ERR_SHAPE;
+  if (!lhs && x_batch < n_pairs) return JQ_ERR_SHAPE;
+  if (n_pairs == 0 || N == 0) return JQ_OK;
+  if (!x || !codes || !scales || !biases || !rhs || !out) return JQ_ERR_NULL;
+  if (!workspace || workspace_bytes < ws_layout(n_pairs, E, M).total) return JQ_ERR_WORKSPACE;
+  if (n_pairs * M > ((int64_t)1 << 30)) return JQ_ERR_SHAPE;
+  hipStream_t st = (hipStream_t)stream;
+  jqk::GatherPlan plan;
+  (void)sorted_indices;  // grouping is done on the device in every case
+  s = build_plan(rhs, n_pairs, E, M, workspace, plan, lhs, st);
+  if (s) return s;
+  plan.x_rows = x_batch * M;
+  jqk::QmmProblem p;
+  p.x = x;
+  p.codes = codes;
+  p.scales = scales;
+  p.biases = biases;
+  p.y = out;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.expert_stride_codes = N * (K * bits / 32);
+  p.expert_stride_sb = N * (K / group_size);
+  return jqk::qmm_gather_launch(p, nullptr, plan, max_tiles_for(n_pairs, E, M), bits, group_size,
+                                x_dtype, sb_dtype, y_dtype, st);
+}
+
+int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E,
+                  const uint32_t* idx, int k, const uint32_t* gate_codes, const void* gate_scales,
+                  const void* gate_biases, const uint32_t* up_codes, const void* up_scales,
+                  const void* up_biases, int bits_gu, const uint32_t* down_codes,
+                  const void* down_scales, const void* down_biases, int bits_d, int sb_dtype,
+                  int group_size, void* h_buf, void* out, int y_dtype, void* workspace,
+                  int64_t workspace_bytes, jq_stream_t stream) {
+  int s = check_expert_shape(bits_gu, group_size, E, I, H);
+  if (s) return s;
+  s = check_expert_shape(bits_d, group_size, E, H, I);
+  if (s) return s;
+  if (x_dtype != JQ_BF16 && x_dtype != JQ_F16) return JQ_ERR_DTYPE;
+  if (!jqh::dtype_ok(sb_dtype) || (y_dtype != JQ_BF16 && y_dtype != JQ_F16)) return JQ_ERR_DTYPE;
+  if (y_dtype != x_dtype) return JQ_ERR_DTYPE;  // h feeds the down projection as activations
+  if (T < 0 || k <= 0) return JQ_ERR_SHAPE;
+  if (H % 128 || I % 128) return JQ_ERR_SHAPE;
+  const int64_t n_pairs = T * k;
+  if (n_pairs == 0) return JQ_OK;
+  if (!x || !idx || !gate_codes || !gate_scales || !gate_biases || !up_codes || !up_scales ||
+      !up_biases || !down_codes || !down_scales || !down_biases || !h_buf || !out)
+    return JQ_ERR_NULL;
+  if (!workspace || workspace_bytes < ws_layout(n_pairs, E, 1).total) return JQ_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  // Pair i = t*k + j uses x row t = i / k and expert idx[i]; one plan serves both launches
+  // (gate+up reads x rows i / k, down reads h rows i).
+  jqk::GatherPlan plan;
+  s = build_plan(idx, n_pairs, E, 1, workspace, plan, nullptr, st);
+  if (s) return s;
+  jqk::GatherPlan plan_gu = plan;
+  plan_gu.lhs = nullptr;
+  plan_gu.pair_div = k;  // x row = pair / k
+  plan_gu.x_rows = T;
+  plan.x_rows = n_pairs;  // down reads h rows = pairs
+  jqk::QmmProblem g, u, d;
+  g.x = x; g.codes = gate_codes; g.scales = gate_scales; g.biases = gate_biases; g.y = h_buf;
+  g.M = 1; g.N = I; g.K = H;
+  g.expert_stride_codes = I * (H * bits_gu / 32);
+  g.expert_stride_sb = I * (H / group_size);
+  u = g;
+  u.codes = up_codes; u.scales = up_scales; u.biases = up_biases;
+  const int64_t mt = max_tiles_for(n_pairs, E, 1);
+  s = jqk::qmm_gather_launch(g, &u, plan_gu, mt, bits_gu, group_size, x_dtype, sb_dtype, y_dtype,
+                             st);
+  if (s) return s;
+  d.x = h_buf; d.codes = down_codes; d.scales = down_scales; d.biases = down_biases; d.y = out;
+  d.M = 1; d.N = H; d.K = I;
+  d.expert_stride_codes = H * (I * bits_d / 32);
+  d.expert_stride_sb = H * (I / group_size);
+  return jqk::qmm_gather_launch(d, nullptr, plan, mt, bits_d, group_size, y_dtype, sb_dtype,
+                                y_dtype, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,67 @@
+// Internal launch descriptors shared by the matmul translation units (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace jqk {
+
+constexpr int kMaxProblems = 8;
+
+struct QmvProblem {
+  const void* x;          // [M, K]
+  const uint32_t* codes;  // [N, K*bits/32]
+  const void* scales;     // [N, K/gs]
+  const void* biases;     // [N, K/gs]
+  void* y;                // [M, N]
+  int64_t N;
+};
+
+struct QmvBatch {
+  QmvProblem p[kMaxProblems];
+  int M;
+  int K;
+};
+
+// Decode GEMV (VALU) for M <= 4, any K % 32 == 0. Returns a jq_status.
+int qmv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
+               hipStream_t st);
+
+// Row-gathered operand description for the grouped (MoE) matrix-core launches.
+// Pairs are processed in expert-grouped order `order`; A row r of segment e is
+//   pair p = order[seg_off[e] + r / M], token row m = r % M
+//   ->  x row (lhs ? lhs[p] : p / pair_div)*M + m
+// and its output goes to out row p*M + m.
+struct GatherPlan {
+  const uint32_t* order;     // [n_pairs] pair ids grouped by expert
+  const int* seg_off;        // [E + 1] segment offsets into order
+  const int4* tiles;         // [max_tiles] (expert, first row, rows, 0)
+  const int* n_tiles;        // [1] number of valid tiles
+  const uint32_t* lhs;       // [n_pairs] or NULL
+  int M;                     // rows per pair
+  int pair_div;              // without lhs: x row of pair p is p / pair_div
+  int64_t x_rows;            // rows of x; a pair mapping outside reads zeros
+};
+
+struct QmmProblem {
+  const void* x;
+  const uint32_t* codes;
+  const void* scales;
+  const void* biases;
+  void* y;
+  int64_t M, N, K;
+  int64_t expert_stride_codes;  // words between experts (gather mode)
+  int64_t expert_stride_sb;     // elements between experts' scale rows (gather mode)
+};
+
+// Matrix-core GEMM y = x @ deq(W)^T. K % 128 == 0 required. Returns a jq_status.
+int qmm_launch(const QmmProblem& p, int bits, int gs, int xd, int sb, int yd, hipStream_t st);
+
+// Grouped matrix-core GEMM over expert segments described by `plan` (device data). With
+// p2 != NULL, p is the gate and p2 the up projection (same shapes) and the output is
+// silu(gate) * up (the SwitchGLU activation).
+int qmm_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPlan& plan,
+                      int64_t max_tiles, int bits, int gs, int xd, int sb, int yd,
+                      hipStream_t st);
+
+}  // namespace jqk

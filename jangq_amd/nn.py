@@ -1,0 +1,157 @@
+"""Module layer mirroring the reference's quantized modules on torch.
+
+  QuantizedLinear / JANGLinear   jang-tools/jang_tools/jangrt/linear.py:22-45 (mlx nn.QuantizedLinear)
+  QuantizedSwitchLinear          mlx_lm switch_layers, as upgraded by loader.py:1826-1848;
+                                 the DSV4.1 SwitchProj (dsv41/model.py:847-857) has the same call
+  SwitchGLU                      mlx_lm SwitchGLU (restated at dots3/ops.py:195-223)
+  SparseMoeBlock                 qwen4_exp/modeling.py:577-599 routing + experts + shared expert
+Parameters are plain tensors (weight uint32, scales/biases bf16 by default) that a loader
+fills; every forward runs the gfx950 kernels through :mod:`jangq_amd.ops`.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+
+class QuantizedLinear(torch.nn.Module):
+    """y = x @ dequantize(weight)^T (+ bias)."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False,
+                 group_size: int = 64, bits: int = 4, *, dtype=torch.bfloat16, device=None):
+        super().__init__()
+        if (in_features * bits) % 32 or in_features % group_size:
+            raise ValueError("in_features must fill whole uint32 words and whole groups")
+        self.in_features, self.out_features = in_features, out_features
+        self.bits, self.group_size, self.mode = bits, group_size, "affine"
+        g = in_features // group_size
+        self.register_buffer("weight", torch.zeros(
+            (out_features, in_features * bits // 32), dtype=torch.int32, device=device))
+        self.register_buffer("scales", torch.zeros((out_features, g), dtype=dtype, device=device))
+        self.register_buffer("biases", torch.zeros((out_features, g), dtype=dtype, device=device))
+        self.bias = (torch.nn.Parameter(torch.zeros(out_features, dtype=dtype, device=device),
+                                        requires_grad=False) if bias else None)
+
+    @classmethod
+    def from_float(cls, w: torch.Tensor, group_size: int = 64, bits: int = 4,
+                   scales_dtype=None) -> "QuantizedLinear":
+        """Quantize a float [out, in] weight on the GPU (mx.quantize rule)."""
+        out_f, in_f = w.shape
+        m = cls(in_f, out_f, group_size=group_size, bits=bits,
+                dtype=scales_dtype or w.dtype, device=w.device)
+        wq, s, b = ops.quantize(w, group_size, bits, scales_dtype=scales_dtype)
+        m.weight = wq.view(torch.int32)
+        m.scales, m.biases = s, b
+        return m
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        y = ops.quantized_matmul(x, self.weight, self.scales, self.biases, True,
+                                 self.group_size, self.bits)
+        return y if self.bias is None else y + self.bias
+
+
+JANGLinear = QuantizedLinear
+
+
+class QuantizedSwitchLinear(torch.nn.Module):
+    """Stacked expert projection: x @ dequantize(weight[indices])^T via gather_qmm."""
+
+    def __init__(self, input_dims: int, output_dims: int, num_experts: int, bias: bool = False,
+                 group_size: int = 64, bits: int = 4, *, dtype=torch.bfloat16, device=None):
+        super().__init__()
+        self.input_dims, self.output_dims, self.num_experts = input_dims, output_dims, num_experts
+        self.bits, self.group_size, self.mode = bits, group_size, "affine"
+        g = input_dims // group_size
+        self.register_buffer("weight", torch.zeros(
+            (num_experts, output_dims, input_dims * bits // 32), dtype=torch.int32, device=device))
+        self.register_buffer("scales", torch.zeros((num_experts, output_dims, g), dtype=dtype,
+                                                   device=device))
+        self.register_buffer("biases", torch.zeros_like(self.scales))
+        self.bias = (torch.nn.Parameter(torch.zeros((num_experts, output_dims), dtype=dtype,
+                                                    device=device), requires_grad=False)
+                     if bias else None)
+
+    def forward(self, x: torch.Tensor, indices: torch.Tensor,
+                sorted_indices: bool = False) -> torch.Tensor:
+        y = ops.gather_qmm(x, self.weight, self.scales, self.biases, rhs_indices=indices,
+                           transpose=True, group_size=self.group_size, bits=self.bits,
+                           sorted_indices=sorted_indices)
+        if self.bias is not None:
+            y = y + self.bias[indices.long()].unsqueeze(-2)
+        return y
+
+    def as_tuple(self):
+        return (self.weight, self.scales, self.biases, self.bits)
+
+
+class SwitchGLU(torch.nn.Module):
+    """down(silu(gate(x)) * up(x)) per selected expert; returns [..., k, hidden]."""
+
+    def __init__(self, input_dims: int, hidden_dims: int, num_experts: int,
+                 group_size: int = 64, bits: int = 4, down_bits: int | None = None, *,
+                 dtype=torch.bfloat16, device=None):
+        super().__init__()
+        kw = dict(group_size=group_size, dtype=dtype, device=device)
+        self.gate_proj = QuantizedSwitchLinear(input_dims, hidden_dims, num_experts, bits=bits, **kw)
+        self.up_proj = QuantizedSwitchLinear(input_dims, hidden_dims, num_experts, bits=bits, **kw)
+        self.down_proj = QuantizedSwitchLinear(hidden_dims, input_dims, num_experts,
+                                               bits=down_bits or bits, **kw)
+
+    def forward(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        return ops.switch_glu(x, indices, self.gate_proj.as_tuple(), self.up_proj.as_tuple(),
+                              self.down_proj.as_tuple(), self.gate_proj.group_size)
+
+
+class SharedExpertMLP(torch.nn.Module):
+    """Dense SwiGLU MLP of quantized linears (the shared expert)."""
+
+    def __init__(self, dims: int, hidden: int, group_size: int = 64, bits: int = 8, *,
+                 dtype=torch.bfloat16, device=None):
+        super().__init__()
+        kw = dict(group_size=group_size, bits=bits, dtype=dtype, device=device)
+        self.gate_proj = QuantizedLinear(dims, hidden, **kw)
+        self.up_proj = QuantizedLinear(dims, hidden, **kw)
+        self.down_proj = QuantizedLinear(hidden, dims, **kw)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        g, u = ops.quantized_matmul_multi(x, [
+            (self.gate_proj.weight, self.gate_proj.scales, self.gate_proj.biases,
+             self.gate_proj.group_size, self.gate_proj.bits),
+            (self.up_proj.weight, self.up_proj.scales, self.up_proj.biases,
+             self.up_proj.group_size, self.up_proj.bits)])
+        h = (torch.nn.functional.silu(g.float()) * u.float()).to(x.dtype)
+        return self.down_proj(h)
+
+
+class SparseMoeBlock(torch.nn.Module):
+    """Router (quantized gate) -> softmax top-k -> SwitchGLU -> weighted sum (+ shared)."""
+
+    def __init__(self, dims: int, expert_hidden: int, num_experts: int, top_k: int, *,
+                 norm_topk_prob: bool = True, shared_hidden: int | None = None,
+                 group_size: int = 64, bits: int = 2, router_bits: int = 8,
+                 shared_bits: int = 8, shared_group_size: int = 64, dtype=torch.bfloat16,
+                 device=None):
+        super().__init__()
+        self.top_k, self.norm_topk_prob = top_k, norm_topk_prob
+        self.gate = QuantizedLinear(dims, num_experts, group_size=64, bits=router_bits,
+                                    dtype=dtype, device=device)
+        self.switch_mlp = SwitchGLU(dims, expert_hidden, num_experts, group_size=group_size,
+                                    bits=bits, dtype=dtype, device=device)
+        self.shared_expert = (SharedExpertMLP(dims, shared_hidden, shared_group_size, shared_bits,
+                                              dtype=dtype, device=device)
+                              if shared_hidden else None)
+
+    def route(self, x: torch.Tensor):
+        logits = self.gate(x).float()
+        return ops.moe_route(logits, self.top_k, self.norm_topk_prob)
+
+    def forward(self, x: torch.Tensor, logits: torch.Tensor | None = None) -> torch.Tensor:
+        if logits is None:
+            logits = self.gate(x).float()
+        inds, scores = ops.moe_route(logits, self.top_k, self.norm_topk_prob)
+        y = self.switch_mlp(x, inds)
+        y = (y.float() * scores.unsqueeze(-1)).sum(dim=-2).to(x.dtype)
+        if self.shared_expert is not None:
+            y = y + self.shared_expert(x)
+        return y

@@ -1,0 +1,319 @@
+"""Operator API of the quantized-weight matmul path, mirroring MLX's affine operators.
+
+Signatures follow the calls the reference makes:
+  quantized_matmul  jang-tools/jang_tools/jangrt/linear.py:41-45, dots3/ops.py:44-51
+  gather_qmm        jang-tools/jang_tools/dsv41/model.py:855-857, dots3/ops.py:168-192
+  dequantize        jang-tools/jang_tools/loader.py:469, tests/mimo_v2_affine_codec_test.py:30-38
+  quantize          jang-tools/jang_tools/convert.py:622-632 (mx.quantize), affine.py:193-276
+Arrays are torch tensors on the GPU; every operator runs a gfx950 kernel of
+``libjangq_amd.so`` on the current stream. Shapes and dtypes are checked here; the C ABI
+re-validates and its error codes surface as ValueError.
+"""
+from __future__ import annotations
+
+import ctypes as _ctypes
+import math
+
+import torch
+
+from . import _lib
+from ._lib import JQ_BF16, JQ_F16, JQ_F32
+
+SUPPORTED_BITS = (2, 3, 4, 5, 6, 8)
+SUPPORTED_GROUP_SIZES = (32, 64, 128)
+
+_DT = {torch.float32: JQ_F32, torch.bfloat16: JQ_BF16, torch.float16: JQ_F16}
+
+
+def _dtype_code(t: torch.Tensor, what: str) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise ValueError(f"{what}: unsupported dtype {t.dtype}") from None
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _dev(t: torch.Tensor, what: str) -> torch.Tensor:
+    """Contiguous GPU operand whose base address is 16-byte aligned (the kernels issue
+    16-byte vector loads from it)."""
+    if not t.is_cuda:
+        raise ValueError(f"{what} must be a GPU tensor (got {t.device})")
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _codes(w: torch.Tensor) -> torch.Tensor:
+    if w.dtype not in (torch.uint32, torch.int32):
+        raise ValueError(f"packed weight must be uint32 (got {w.dtype})")
+    return _dev(w, "packed weight")
+
+
+def _check_mode(mode: str, transpose: bool) -> None:
+    if mode != "affine":
+        raise ValueError(f"mode={mode!r}: only the affine mode is implemented")
+    if not transpose:
+        raise ValueError("transpose=False is not supported (every reference call uses transpose=True)")
+
+
+def _check_bits_gs(bits: int, group_size: int) -> None:
+    if bits not in SUPPORTED_BITS:
+        raise ValueError(f"unsupported bits={bits}; expected one of {SUPPORTED_BITS}")
+    if group_size not in SUPPORTED_GROUP_SIZES:
+        raise ValueError(
+            f"unsupported group_size={group_size}; expected one of {SUPPORTED_GROUP_SIZES}")
+
+
+def packed_in_features(w: torch.Tensor, bits: int) -> int:
+    """Logical input dimension K of a packed weight: last dim * 32 / bits."""
+    return w.shape[-1] * 32 // bits
+
+
+def unpack(w: torch.Tensor, bits: int) -> torch.Tensor:
+    """Codes as uint8 [..., K] (pack.py:85-149 applied row-wise to a uint32 matrix)."""
+    if bits not in SUPPORTED_BITS:
+        raise ValueError(f"unsupported bits={bits}")
+    w = _codes(w)
+    K = packed_in_features(w, bits)
+    if (w.shape[-1] * 32) % bits:
+        raise ValueError("packed width is not a whole number of codes")
+    rows = math.prod(w.shape[:-1])
+    out = torch.empty((*w.shape[:-1], K), dtype=torch.uint8, device=w.device)
+    _lib.check(_lib.lib().jq_unpack(_ptr(w), bits, rows, K, _ptr(out), _stream()), "unpack")
+    return out
+
+
+def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               group_size: int = 64, bits: int = 4, mode: str = "affine",
+               dtype: torch.dtype | None = None) -> torch.Tensor:
+    """W = q*scale + bias per group, fp32 arithmetic, returned as ``dtype`` (default
+    scales.dtype, as mx.dequantize). 2-D or stacked [E, N, P] weights."""
+    _check_mode(mode, True)
+    _check_bits_gs(bits, group_size)
+    w = _codes(w)
+    scales = _dev(scales, "scales")
+    biases = _dev(biases, "biases")
+    K = packed_in_features(w, bits)
+    if scales.shape != biases.shape or scales.shape[:-1] != w.shape[:-1]:
+        raise ValueError(f"shape mismatch: w {tuple(w.shape)}, scales {tuple(scales.shape)}, "
+                         f"biases {tuple(biases.shape)}")
+    if scales.shape[-1] * group_size != K:
+        raise ValueError(f"scales width {scales.shape[-1]} x group_size {group_size} != K {K}")
+    if scales.dtype != biases.dtype:
+        raise ValueError("scales and biases must share a dtype")
+    out_dtype = dtype or scales.dtype
+    rows = math.prod(w.shape[:-1])
+    out = torch.empty((*w.shape[:-1], K), dtype=out_dtype, device=w.device)
+    _lib.check(_lib.lib().jq_dequantize(
+        _ptr(w), _ptr(scales), _ptr(biases), _dtype_code(scales, "scales"), bits, group_size,
+        rows, K, _ptr(out), _dtype_code(out, "output"), _stream()), "dequantize")
+    return out
+
+
+def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4, mode: str = "affine",
+             scales_dtype: torch.dtype | None = None):
+    """Affine group quantization with mx.quantize's rule. Returns (w_q uint32 [..., K*bits/32],
+    scales, biases) with scales/biases in ``scales_dtype`` (default w.dtype, as MLX)."""
+    _check_mode(mode, True)
+    _check_bits_gs(bits, group_size)
+    w = _dev(w, "weights")
+    K = w.shape[-1]
+    if K % group_size:
+        raise ValueError(f"input dimension {K} is not divisible by group_size={group_size}")
+    sdt = scales_dtype or w.dtype
+    rows = math.prod(w.shape[:-1])
+    lead = tuple(w.shape[:-1])
+    wq = torch.empty((*lead, K * bits // 32), dtype=torch.int32, device=w.device)
+    scales = torch.empty((*lead, K // group_size), dtype=sdt, device=w.device)
+    biases = torch.empty_like(scales)
+    _lib.check(_lib.lib().jq_quantize(
+        _ptr(w), _dtype_code(w, "weights"), bits, group_size, rows, K, _ptr(wq), _ptr(scales),
+        _ptr(biases), _dtype_code(scales, "scales"), _stream()), "quantize")
+    return wq.view(torch.uint32), scales, biases
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: torch.Tensor, transpose: bool = True, group_size: int = 64,
+                     bits: int = 4, mode: str = "affine", *,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x @ dequantize(w)^T with fp32 accumulation; y has x's dtype and shape [..., N]."""
+    _check_mode(mode, transpose)
+    _check_bits_gs(bits, group_size)
+    if biases is None:
+        raise ValueError("affine mode needs biases")
+    x = _dev(x, "x")
+    w = _codes(w)
+    scales = _dev(scales, "scales")
+    biases = _dev(biases, "biases")
+    if w.dim() != 2:
+        raise ValueError(f"quantized_matmul expects a 2-D packed weight, got {tuple(w.shape)}")
+    N = w.shape[0]
+    K = packed_in_features(w, bits)
+    if x.shape[-1] != K:
+        raise ValueError(f"x last dim {x.shape[-1]} != K {K} (w {tuple(w.shape)}, bits {bits})")
+    if tuple(scales.shape) != (N, K // group_size) or scales.shape != biases.shape:
+        raise ValueError(f"scales/biases must be {(N, K // group_size)}, got "
+                         f"{tuple(scales.shape)} / {tuple(biases.shape)}")
+    M = math.prod(x.shape[:-1])
+    if out is None:
+        out = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().jq_quantized_matmul(
+        _ptr(x), _dtype_code(x, "x"), _ptr(w), _ptr(scales), _ptr(biases),
+        _dtype_code(scales, "scales"), bits, group_size, M, N, K, _ptr(out),
+        _dtype_code(out, "output"), _stream()), "quantized_matmul")
+    return out
+
+
+def quantized_matmul_multi(x: torch.Tensor, weights, *, outs=None):
+    """Several projections of the same x (q/k/v, gate/up) in one launch where they share
+    bits, group_size and K; ``weights`` is a sequence of (w, scales, biases, group_size,
+    bits). Returns the list of outputs [..., N_i] in x.dtype."""
+    x = _dev(x, "x")
+    n = len(weights)
+    K = x.shape[-1]
+    M = math.prod(x.shape[:-1])
+    keep, ys, ws, ss, bs, bits_l, gs_l, ns = [], [], [], [], [], [], [], []
+    for i, (w, s, b, gs, bits) in enumerate(weights):
+        _check_bits_gs(bits, gs)
+        w, s, b = _codes(w), _dev(s, "scales"), _dev(b, "biases")
+        if packed_in_features(w, bits) != K:
+            raise ValueError(f"weight {i}: K mismatch")
+        if s.dtype != weights[0][1].dtype:
+            raise ValueError("all scales must share a dtype")
+        y = outs[i] if outs is not None else torch.empty(
+            (*x.shape[:-1], w.shape[0]), dtype=x.dtype, device=x.device)
+        keep += [w, s, b]
+        ys.append(y)
+        ws.append(w.data_ptr()); ss.append(s.data_ptr()); bs.append(b.data_ptr())
+        bits_l.append(bits); gs_l.append(gs); ns.append(w.shape[0])
+    ptrs = lambda vals: (_ctypes.c_void_p * n)(*vals)  # noqa: E731
+    st = _lib.lib().jq_quantized_matmul_multi(
+        n, ptrs([x.data_ptr()] * n), _dtype_code(x, "x"), ptrs(ws), ptrs(ss), ptrs(bs),
+        _dtype_code(weights[0][1], "scales"), (_ctypes.c_int * n)(*bits_l),
+        (_ctypes.c_int * n)(*gs_l), (_ctypes.c_int64 * n)(*([M] * n)),
+        (_ctypes.c_int64 * n)(*ns), (_ctypes.c_int64 * n)(*([K] * n)),
+        ptrs([y.data_ptr() for y in ys]), _dtype_code(x, "output"), _stream())
+    _lib.check(st, "quantized_matmul_multi")
+    return ys
+
+
+def _gather_workspace(n_pairs: int, E: int, M: int, device) -> torch.Tensor:
+    size = _lib.lib().jq_gather_workspace_size(n_pairs, E, M)
+    if size < 0:
+        raise ValueError("invalid gather workspace request")
+    return torch.empty(max(size, 256), dtype=torch.uint8, device=device)
+
+
+def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+               biases: torch.Tensor | None = None, lhs_indices: torch.Tensor | None = None,
+               rhs_indices: torch.Tensor | None = None, transpose: bool = True,
+               group_size: int = 64, bits: int = 4, mode: str = "affine",
+               sorted_indices: bool = False) -> torch.Tensor:
+    """out[i] = x[lhs[i]] @ dequantize(w[rhs[i]])^T, MLX broadcasting rules.
+
+    x [*B, M, K]; w [E, N, P]; lhs indexes the flattened batch of x (default: every batch
+    entry, broadcast against rhs); rhs indexes experts (default: arange(E)).
+    Output [*broadcast(lhs, rhs), M, N] in x.dtype."""
+    _check_mode(mode, transpose)
+    _check_bits_gs(bits, group_size)
+    if biases is None:
+        raise ValueError("affine mode needs biases")
+    x = _dev(x, "x")
+    w = _codes(w)
+    scales = _dev(scales, "scales")
+    biases = _dev(biases, "biases")
+    if w.dim() != 3:
+        raise ValueError(f"gather_qmm expects stacked weights [E, N, P], got {tuple(w.shape)}")
+    if x.dim() < 2:
+        raise ValueError("x must have at least 2 dims [..., M, K]")
+    E, N = w.shape[0], w.shape[1]
+    K = packed_in_features(w, bits)
+    if x.shape[-1] != K:
+        raise ValueError(f"x last dim {x.shape[-1]} != K {K}")
+    if tuple(scales.shape) != (E, N, K // group_size) or scales.shape != biases.shape:
+        raise ValueError("scales/biases shape mismatch")
+    M = x.shape[-2]
+    bshape = tuple(x.shape[:-2])
+    Bx = math.prod(bshape)
+    dev = x.device
+    if lhs_indices is None:
+        lhs_indices = torch.arange(Bx, device=dev, dtype=torch.int32).reshape(bshape)
+    if rhs_indices is None:
+        rhs_indices = torch.arange(E, device=dev, dtype=torch.int32)
+    lhs_b, rhs_b = torch.broadcast_tensors(lhs_indices.to(dev), rhs_indices.to(dev))
+    ishape = tuple(lhs_b.shape)
+    lhs_f = lhs_b.reshape(-1).to(torch.int32).contiguous()
+    rhs_f = rhs_b.reshape(-1).to(torch.int32).contiguous()
+    n_pairs = lhs_f.numel()
+    out = torch.empty((*ishape, M, N), dtype=x.dtype, device=dev)
+    if n_pairs == 0:
+        return out
+    ws = _gather_workspace(n_pairs, E, M, dev)
+    _lib.check(_lib.lib().jq_gather_qmm(
+        _ptr(x), _dtype_code(x, "x"), Bx, M, _ptr(w), _ptr(scales), _ptr(biases),
+        _dtype_code(scales, "scales"), bits, group_size, E, N, K, _ptr(lhs_f), _ptr(rhs_f),
+        n_pairs, int(sorted_indices), _ptr(out), _dtype_code(out, "output"), _ptr(ws),
+        ws.numel(), _stream()), "gather_qmm")
+    return out
+
+
+def moe_route(logits: torch.Tensor, k: int, renorm: bool = True):
+    """softmax(logits) in fp32 -> top-k ids (descending) and their probabilities,
+    optionally renormalised to sum 1 (qwen4_exp/modeling.py:587-593)."""
+    logits = _dev(logits, "logits")
+    if logits.dtype != torch.float32:
+        logits = logits.float()
+    E = logits.shape[-1]
+    T = math.prod(logits.shape[:-1])
+    idx = torch.empty((*logits.shape[:-1], k), dtype=torch.int32, device=logits.device)
+    wts = torch.empty((*logits.shape[:-1], k), dtype=torch.float32, device=logits.device)
+    _lib.check(_lib.lib().jq_moe_route(_ptr(logits), T, E, k, int(renorm), _ptr(idx), _ptr(wts),
+                                       _stream()), "moe_route")
+    return idx, wts
+
+
+def switch_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, down, group_size: int = 64):
+    """SwitchGLU over stacked experts (mlx_lm SwitchGLU.__call__, restated at
+    dots3/ops.py:195-223): out[..., j, :] = down_e(silu(gate_e(x)) * up_e(x)), e = indices[..., j].
+
+    gate/up/down are (w, scales, biases, bits) tuples of stacked expert weights. One grouped
+    launch computes gate+up+SiLU for every active expert, a second the down projection."""
+    x = _dev(x, "x")
+    indices = _dev(indices, "indices")
+    gw, gsc, gb, bits_gu = gate
+    uw, usc, ub, bits_u = up
+    dw, dsc, db, bits_d = down
+    if bits_u != bits_gu:
+        raise ValueError("gate and up projections must share a bit width")
+    _check_bits_gs(bits_gu, group_size)
+    _check_bits_gs(bits_d, group_size)
+    gw, uw, dw = _codes(gw), _codes(uw), _codes(dw)
+    E, I = gw.shape[0], gw.shape[1]
+    H = x.shape[-1]
+    k = indices.shape[-1]
+    if packed_in_features(gw, bits_gu) != H or dw.shape[1] != H or packed_in_features(dw, bits_d) != I:
+        raise ValueError("expert weight shapes do not match x / each other")
+    T = math.prod(x.shape[:-1])
+    if math.prod(indices.shape[:-1]) != T:
+        raise ValueError("indices leading dims must match x")
+    idx = indices.reshape(T, k).to(torch.int32).contiguous()
+    h = torch.empty((T * k, I), dtype=x.dtype, device=x.device)
+    out = torch.empty((*x.shape[:-1], k, H), dtype=x.dtype, device=x.device)
+    ws = _gather_workspace(T * k, E, 1, x.device)
+    sdt = _dtype_code(gsc, "scales")
+    _lib.check(_lib.lib().jq_switch_glu(
+        _ptr(x), _dtype_code(x, "x"), T, H, I, E, _ptr(idx), k,
+        _ptr(gw), _ptr(_dev(gsc, "scales")), _ptr(_dev(gb, "biases")),
+        _ptr(uw), _ptr(_dev(usc, "scales")), _ptr(_dev(ub, "biases")), bits_gu,
+        _ptr(dw), _ptr(_dev(dsc, "scales")), _ptr(_dev(db, "biases")), bits_d, sdt, group_size,
+        _ptr(h), _ptr(out), _dtype_code(out, "output"), _ptr(ws), ws.numel(), _stream()),
+        "switch_glu")
+    return out

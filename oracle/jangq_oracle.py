@@ -1,0 +1,268 @@
+"""CPU oracle for the quantized-weight matmul path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+use this module, and only as the checker / the timed CPU baseline. The product
+(``jangq_amd``) never imports it.
+
+Each function restates one reference algorithm (file:line relative to the reference
+checkout) in numpy:
+
+  pack_bits / unpack_bits      jang-tools/jang_tools/pack.py:12-82 / 85-149
+  pack_rows / unpack_rows      the same stream viewed as uint32 rows (affine.py:256-265, 457)
+  quantize_affine              jang-tools/jang_tools/affine.py:193-276 (mirror of mx.quantize)
+  dequantize_affine            jang-tools/jang_tools/affine.py:445-463 (+ 3-D flattening of
+                               quantize.py:238-239)
+  quantized_matmul             mx.quantized_matmul contract, jangrt/linear.py:41-45
+  gather_qmm                   naive per-pair loop of jang_tools/dots3/ops_selftest.py:18-28
+  switch_glu                   mlx_lm SwitchGLU as restated at dots3/ops.py:195-223
+  route_topk                   qwen4_exp/modeling.py:587-593
+
+How each is pinned (tests/test_oracle.py):
+  pack/unpack       known answers of jang-tools/tests/test_pack.py:33-61, the LSB-first 3-bit
+                    straddle vector, round trips with the reference test seeds, and a
+                    bit-by-bit C restatement (oracle/jq_oracle.c) agreeing on random data
+  quantize_affine   the MLX-produced fixture jang-runtime/Tests/JANGCoreMetalTests/fixtures/
+                    matmul_4bit_64x128.safetensors (codes, f16 sidecars) regenerated from
+                    its seed; invariants (codes in range, edge code hits the edge)
+  dequantize        the same fixture's y_ref (MLX dequantize @ x), dequant(s=1,b=0) == q,
+                    two-rounding vs fused-FMA discrimination, C restatement agreement
+  quantized_matmul  fixture y_ref; brute-force pure-Python loop on tiny shapes
+  gather/switch     brute force on tiny shapes; sorted/unsorted equivalence
+  route_topk        brute force (full sort) on small shapes
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+SUPPORTED_BITS = (2, 3, 4, 5, 6, 8)
+
+# ----------------------------------------------------------------------------- bf16 / f16
+
+
+def f32_to_bf16_bits(a) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bit patterns (NaN -> 0x7FC0)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    return np.where(nan, np.uint16(0x7FC0), r)
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(a) -> np.ndarray:
+    """fp32 value of the bf16 rounding of a."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(a))
+
+
+def round_to(a, dtype: str) -> np.ndarray:
+    a = np.asarray(a, dtype=np.float32)
+    if dtype == "bf16":
+        return round_bf16(a)
+    if dtype == "f16":
+        return a.astype(np.float16).astype(np.float32)
+    return a
+
+
+# ----------------------------------------------------------------------------- bit stream
+
+
+def pack_bits(values, bits: int) -> np.ndarray:
+    """LSB-first stream: value i occupies bits [i*bits, (i+1)*bits); (n*bits+7)//8 bytes."""
+    v = np.asarray(values, dtype=np.uint64).reshape(-1)
+    if v.size and int(v.max()) >= (1 << bits):
+        raise ValueError("value does not fit the bit width")
+    bitplanes = ((v[:, None] >> np.arange(bits, dtype=np.uint64)[None, :]) & 1).astype(np.uint8)
+    return np.packbits(bitplanes.reshape(-1), bitorder="little")
+
+
+def unpack_bits(packed, bits: int, count: int) -> np.ndarray:
+    """Inverse of pack_bits; any array shape is flattened as its row-major byte stream."""
+    b = np.asarray(packed, dtype=np.uint8).reshape(-1)
+    stream = np.unpackbits(b, bitorder="little")[: count * bits]
+    planes = stream.reshape(count, bits).astype(np.uint16)
+    return (planes << np.arange(bits, dtype=np.uint16)[None, :]).sum(axis=1).astype(np.uint8)
+
+
+def pack_rows(codes: np.ndarray, bits: int) -> np.ndarray:
+    """Codes [rows, K] -> uint32 [rows, K*bits/32] (each row is a whole number of words)."""
+    codes = np.asarray(codes)
+    rows, K = codes.shape
+    if (K * bits) % 32:
+        raise ValueError("row is not a whole number of uint32 words")
+    return pack_bits(codes.reshape(-1), bits).view(np.uint32).reshape(rows, K * bits // 32)
+
+
+def unpack_rows(w: np.ndarray, bits: int) -> np.ndarray:
+    """uint32 [..., P] -> codes uint8 [..., P*32/bits]."""
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    K = w.shape[-1] * 32 // bits
+    rows = int(np.prod(w.shape[:-1]))
+    return unpack_bits(w.view(np.uint8), bits, rows * K).reshape(*w.shape[:-1], K)
+
+
+# ----------------------------------------------------------------------------- quantizer
+
+_FP16_TINY = np.float32(np.finfo(np.float16).smallest_normal)
+
+
+def _to_f16_nonzero(scale: np.ndarray) -> np.ndarray:
+    safe = np.where(np.abs(scale) < _FP16_TINY,
+                    np.copysign(_FP16_TINY, np.where(scale == 0, 1.0, scale)), scale)
+    return safe.astype(np.float16)
+
+
+def quantize_affine(w, bits: int, group_size: int, sidecar: str = "bf16",
+                    input_via_f16: bool = False):
+    """mx.quantize affine rule. Returns (packed u32 [rows, K*bits/32], scales, biases, codes).
+
+    sidecar: "bf16" (uint16 bf16 bit patterns), "f16" (np.float16 with the non-zero guard of
+    affine.py:43-51) or "f32". input_via_f16 reproduces affine.py:212 (source cast to f16)."""
+    if bits not in SUPPORTED_BITS:
+        raise ValueError(f"unsupported bits={bits}")
+    src = np.asarray(w)
+    if input_via_f16:
+        src = src.astype(np.float16)
+    src = src.astype(np.float32)
+    rows, K = src.shape
+    if K % group_size:
+        raise ValueError("K not divisible by group_size")
+    g = src.reshape(rows, K // group_size, group_size)
+    bins = np.float32((1 << bits) - 1)
+    low = g.min(axis=-1)
+    high = np.maximum(g.max(axis=-1), np.float32(0.0))
+    scale = np.maximum((high - low) / bins, np.float32(1e-7)).astype(np.float32)
+    dominant_low = np.abs(low) > np.abs(high)
+    scale = np.where(dominant_low, scale, -scale).astype(np.float32)
+    edge = np.where(dominant_low, low, high).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        edge_code = np.rint(edge / scale).astype(np.float32)
+        at_zero = edge_code == 0
+        refined = np.where(at_zero, scale, edge / np.where(at_zero, 1, edge_code)).astype(np.float32)
+    scale = np.where(at_zero, scale, refined).astype(np.float32)
+    bias = np.where(at_zero, np.float32(0.0), edge).astype(np.float32)
+    q = np.rint((g - bias[..., None]) / scale[..., None])
+    codes = np.clip(q, 0, bins).astype(np.uint8).reshape(rows, K)
+    packed = pack_rows(codes, bits)
+    if sidecar == "bf16":
+        s_out, b_out = f32_to_bf16_bits(scale), f32_to_bf16_bits(bias)
+    elif sidecar == "f16":
+        s_out, b_out = _to_f16_nonzero(scale), bias.astype(np.float16)
+    else:
+        s_out, b_out = scale, bias
+    return packed, s_out, b_out, codes
+
+
+def sidecar_f32(a, sidecar: str) -> np.ndarray:
+    """Stored sidecar as fp32 values."""
+    if sidecar == "bf16":
+        return bf16_bits_to_f32(a)
+    return np.asarray(a).astype(np.float32)
+
+
+# ----------------------------------------------------------------------------- dequant
+
+
+def dequantize_affine(w, scales_f32, biases_f32, bits: int, group_size: int) -> np.ndarray:
+    """fl(fl(q*s) + b) in fp32; w [..., P] (2-D or stacked), scales/biases fp32 [..., G]."""
+    codes = unpack_rows(w, bits).astype(np.float32)
+    lead = codes.shape[:-1]
+    K = codes.shape[-1]
+    q = codes.reshape(*lead, K // group_size, group_size)
+    s = np.asarray(scales_f32, dtype=np.float32)[..., None]
+    b = np.asarray(biases_f32, dtype=np.float32)[..., None]
+    prod = (q * s).astype(np.float32)          # first rounding
+    return (prod + b).astype(np.float32).reshape(*lead, K)  # second rounding
+
+
+# ----------------------------------------------------------------------------- matmuls
+
+
+def quantized_matmul(x_f32, w, s_f32, b_f32, bits: int, group_size: int) -> np.ndarray:
+    """y = x @ dequant(W)^T accumulated in fp64 (x given as fp32 values). Returns fp64."""
+    W = dequantize_affine(w, s_f32, b_f32, bits, group_size).astype(np.float64)
+    x = np.asarray(x_f32, dtype=np.float64)
+    return x @ W.T
+
+
+def gather_qmm(x_f32, w, s_f32, b_f32, lhs, rhs, bits: int, group_size: int) -> np.ndarray:
+    """out[i] = x[lhs[i]] @ dequant(W[rhs[i]])^T, fp64; x [B, M, K], w [E, N, P]."""
+    x = np.asarray(x_f32, dtype=np.float64)
+    lhs = np.asarray(lhs).reshape(-1)
+    rhs = np.asarray(rhs).reshape(-1)
+    E, N = w.shape[0], w.shape[1]
+    out = np.zeros((lhs.size, x.shape[-2], N), dtype=np.float64)
+    cache = {}
+    for i, (l, r) in enumerate(zip(lhs, rhs)):
+        if r not in cache:
+            cache[r] = dequantize_affine(w[r], s_f32[r], b_f32[r], bits, group_size).astype(np.float64)
+        out[i] = x[l] @ cache[r].T
+    return out
+
+
+def silu(v):
+    v = np.asarray(v, dtype=np.float64)
+    return v / (1.0 + np.exp(-v))
+
+
+def switch_glu(x_f32, idx, gate, up, down, group_size: int, out_dtype: str = "bf16"):
+    """Per (token t, slot j), e = idx[t, j]:
+    g, u = round(x[t] @ Wg[e]^T), round(x[t] @ Wu[e]^T); h = round(silu(g) * u);
+    out[t, j] = round(h @ Wd[e]^T). Each matmul accumulates in fp64. gate/up/down are
+    (w, s_f32, b_f32, bits). Returns out (fp32 values of the rounded results) and h."""
+    x = np.asarray(x_f32, dtype=np.float64)
+    idx = np.asarray(idx)
+    T, k = idx.shape
+    deq = {}
+
+    def W(which, e):
+        key = (which, int(e))
+        if key not in deq:
+            w, s, b, bits = {"g": gate, "u": up, "d": down}[which]
+            deq[key] = dequantize_affine(w[e], s[e], b[e], bits, group_size).astype(np.float64)
+        return deq[key]
+
+    H = x.shape[-1]
+    I = gate[0].shape[1]
+    out = np.zeros((T, k, H), dtype=np.float32)
+    hs = np.zeros((T, k, I), dtype=np.float32)
+    for t in range(T):
+        for j in range(k):
+            e = idx[t, j]
+            g = round_to(x[t] @ W("g", e).T, out_dtype).astype(np.float64)
+            u = round_to(x[t] @ W("u", e).T, out_dtype).astype(np.float64)
+            h = round_to(silu(g) * u, out_dtype)
+            hs[t, j] = h
+            out[t, j] = round_to(h.astype(np.float64) @ W("d", e).T, out_dtype)
+    return out, hs
+
+
+def route_topk(logits, k: int, renorm: bool = True):
+    """softmax in fp64, top-k by descending probability (ties: lower id first)."""
+    z = np.asarray(logits, dtype=np.float64)
+    z = z - z.max(axis=-1, keepdims=True)
+    p = np.exp(z)
+    p /= p.sum(axis=-1, keepdims=True)
+    order = np.lexsort((np.arange(p.shape[-1])[None, :].repeat(p.shape[0], 0), -p), axis=-1)
+    idx = order[:, :k]
+    w = np.take_along_axis(p, idx, axis=-1)
+    if renorm:
+        w = w / w.sum(axis=-1, keepdims=True)
+    return idx.astype(np.int64), w
+
+
+# ----------------------------------------------------------------------------- metrics
+
+
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    den = math.sqrt(float((b * b).sum()))
+    return math.sqrt(float(((a - b) ** 2).sum())) / (den if den > 0 else 1.0)
+
+
+def max_abs(a, b) -> float:
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64)), initial=0.0))

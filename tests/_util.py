@@ -1,0 +1,79 @@
+"""Helpers shared by the GPU parity tests: seeded inputs built with the CPU oracle and
+moved to the device, and the tolerance checks the north star states."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import jangq_oracle as O
+
+# Matmul outputs vs the fp32-accumulated oracle rounded to the output dtype.
+REL_L2_TOL = 1e-3
+MAX_ABS_TOL = 2e-2
+
+
+def bf16_tensor(a_f32: np.ndarray, device="cuda") -> torch.Tensor:
+    bits = O.f32_to_bf16_bits(a_f32)
+    return torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).to(device)
+
+
+def to_tensor(a: np.ndarray, dtype: str, device="cuda") -> torch.Tensor:
+    """fp32 values -> device tensor of dtype ("bf16", "f16", "f32")."""
+    if dtype == "bf16":
+        return bf16_tensor(a, device)
+    if dtype == "f16":
+        return torch.from_numpy(np.asarray(a, np.float32).astype(np.float16)).to(device)
+    return torch.from_numpy(np.asarray(a, np.float32)).to(device)
+
+
+def sidecar_tensor(a, sidecar: str, device="cuda") -> torch.Tensor:
+    if sidecar == "bf16":
+        return torch.from_numpy(np.asarray(a, np.uint16).view(np.int16).copy()).view(
+            torch.bfloat16).to(device)
+    if sidecar == "f16":
+        return torch.from_numpy(np.asarray(a, np.float16)).to(device)
+    return torch.from_numpy(np.asarray(a, np.float32)).to(device)
+
+
+def codes_tensor(packed: np.ndarray, device="cuda") -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(packed).view(np.int32)).to(device)
+
+
+def values_of(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+class QWeight:
+    """A seeded quantized matrix (or expert stack) on host and device."""
+
+    def __init__(self, rows, K, bits, gs, seed, sidecar="bf16", std=0.02, experts=None,
+                 device="cuda"):
+        rng = np.random.default_rng(seed)
+        shape = (rows, K) if experts is None else (experts * rows, K)
+        w = O.round_bf16(rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+        packed, s, b, codes = O.quantize_affine(w, bits, gs, sidecar=sidecar)
+        if experts is not None:
+            packed = packed.reshape(experts, rows, -1)
+            s = s.reshape(experts, rows, -1)
+            b = b.reshape(experts, rows, -1)
+            codes = codes.reshape(experts, rows, -1)
+        self.bits, self.gs, self.sidecar = bits, gs, sidecar
+        self.packed, self.codes = packed, codes
+        self.s_raw, self.b_raw = s, b
+        self.s = O.sidecar_f32(s, sidecar)
+        self.b = O.sidecar_f32(b, sidecar)
+        self.dw = codes_tensor(packed, device)
+        self.ds = sidecar_tensor(s, sidecar, device)
+        self.db = sidecar_tensor(b, sidecar, device)
+
+    def dequant(self):
+        return O.dequantize_affine(self.packed, self.s, self.b, self.bits, self.gs)
+
+
+def assert_close(got: np.ndarray, ref: np.ndarray, what: str,
+                 rel=REL_L2_TOL, mabs=MAX_ABS_TOL):
+    r = O.rel_l2(got, ref)
+    m = O.max_abs(got, ref)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    assert r <= rel and m <= mabs, f"{what}: rel_l2={r:.3e} (tol {rel}) max_abs={m:.3e} (tol {mabs})"
+    return r, m

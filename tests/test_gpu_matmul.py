@@ -1,0 +1,106 @@
+"""GPU parity of quantized_matmul (decode GEMV and matrix-core GEMM) against the oracle.
+
+Outputs are compared with the oracle's fp64 accumulation of the exactly dequantized
+weights, rounded to the output dtype: rel-L2 <= 1e-3 and max-abs <= 2e-2 (north star);
+fp32 outputs are held to rel-L2 <= 2e-6."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import jangq_amd as jq
+from oracle import jangq_oracle as O
+from tests._util import QWeight, assert_close, codes_tensor, to_tensor, values_of
+
+pytestmark = pytest.mark.gpu
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def run_case(M, N, K, bits, gs, xdt="bf16", sidecar="bf16", seed=0, ydt=None):
+    qw = QWeight(N, K, bits, gs, seed=seed, sidecar=sidecar)
+    rng = np.random.default_rng(seed + 1)
+    x = O.round_to(rng.standard_normal((M, K), dtype=np.float32), xdt)
+    tx = to_tensor(x, xdt)
+    out = None
+    if ydt is not None:
+        out = torch.empty((M, N), dtype={"f32": torch.float32, "bf16": torch.bfloat16,
+                                          "f16": torch.float16}[ydt], device="cuda")
+    y = jq.quantized_matmul(tx, qw.dw, qw.ds, qw.db, True, gs, bits, out=out)
+    ref = O.quantized_matmul(x, qw.packed, qw.s, qw.b, bits, gs)
+    ydt = ydt or xdt
+    if ydt == "f32":
+        return assert_close(values_of(y), ref, f"M{M} N{N} K{K} b{bits} g{gs}", rel=2e-6, mabs=1e-4)
+    return assert_close(values_of(y), O.round_to(ref, ydt), f"M{M} N{N} K{K} b{bits} g{gs} {xdt}")
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("M", [1, 3, 8, 32])
+def test_matmul_bits_groups(bits, gs, M):
+    run_case(M, 96, 512, bits, gs, seed=bits * 10 + gs + M)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 16, 17, 64, 130])
+def test_matmul_m_sweep_fp32_out(M):
+    run_case(M, 200, 1024, 4, 64, seed=M, ydt="f32")
+
+
+@pytest.mark.parametrize("xdt", ["f16", "f32"])
+@pytest.mark.parametrize("M", [1, 6, 40])
+def test_matmul_activation_dtypes(xdt, M):
+    run_case(M, 64, 256, 3, 64, xdt=xdt, sidecar="f16", seed=M + 5)
+
+
+@pytest.mark.parametrize("M,K,gs", [(9, 320, 64), (6, 96, 32), (2, 64, 64)])
+def test_matmul_k_not_multiple_of_tile(M, K, gs):
+    run_case(M, 48, K, 6, gs, seed=K)
+
+
+def test_matmul_empty_and_zero_k():
+    qw = QWeight(8, 64, 4, 64, seed=1)
+    x = torch.zeros((0, 64), dtype=torch.bfloat16, device="cuda")
+    assert jq.quantized_matmul(x, qw.dw, qw.ds, qw.db).shape == (0, 8)
+
+
+def test_matmul_mlx_fixture():
+    """The reference's MLX fixture: 4-bit, gs64, f16 x and sidecars, 64 -> 128."""
+    from safetensors.numpy import load_file
+
+    d = load_file(str(GOLD / "matmul_4bit_64x128.safetensors"))
+    x = torch.from_numpy(d["x"][None]).cuda()
+    w = codes_tensor(d["W.weight"])
+    s = torch.from_numpy(d["W.scales"]).cuda()
+    b = torch.from_numpy(d["W.biases"]).cuda()
+    y = jq.quantized_matmul(x, w, s, b, True, 64, 4, out=torch.empty((1, 128), device="cuda"))
+    got = values_of(y)[0]
+    assert O.max_abs(got, d["y_ref"]) < 1e-2  # QuantizedMatmul4Tests.swift:83-84
+    ref = O.quantized_matmul(d["x"].astype(np.float32)[None], d["W.weight"],
+                             d["W.scales"].astype(np.float32), d["W.biases"].astype(np.float32), 4, 64)
+    assert O.rel_l2(got, ref[0]) < 2e-6
+
+
+@pytest.mark.parametrize("M", [1, 8, 32])
+def test_c1_full_size(M):
+    """Config 1 shape: 4096 x 4096, 4-bit g64 (and the decode batches of config 2)."""
+    run_case(M, 4096, 4096, 4, 64, seed=101 + M)
+
+
+@pytest.mark.parametrize("N,K,bits", [(14336, 4096, 3), (4096, 14336, 2), (1024, 4096, 6)])
+def test_c2_projection_shapes(N, K, bits):
+    run_case(1, N, K, bits, 64, seed=N + bits)
+    run_case(8, N, K, bits, 64, seed=N + bits + 1)
+
+
+def test_multi_matches_single():
+    K = 1024
+    ws = [QWeight(n, K, 6, 64, seed=i) for i, n in enumerate((256, 64, 64))]
+    rng = np.random.default_rng(77)
+    for M in (1, 3, 8):
+        x = O.round_bf16(rng.standard_normal((M, K), dtype=np.float32))
+        tx = to_tensor(x, "bf16")
+        ys = jq.quantized_matmul_multi(tx, [(w.dw, w.ds, w.db, 64, 6) for w in ws])
+        for w, y in zip(ws, ys):
+            single = jq.quantized_matmul(tx, w.dw, w.ds, w.db, True, 64, 6)
+            assert torch.equal(y, single)

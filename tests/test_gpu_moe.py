@@ -1,0 +1,124 @@
+"""GPU parity of the MoE path: router top-k, gather_qmm (device grouping by expert) and the
+fused SwitchGLU launches, against the oracle's per-pair loops."""
+import numpy as np
+import pytest
+import torch
+
+import jangq_amd as jq
+from jangq_amd import nn as jnn
+from oracle import jangq_oracle as O
+from tests._util import QWeight, assert_close, to_tensor, values_of
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("T,E,k", [(1, 128, 4), (16, 128, 4), (64, 128, 4), (32, 512, 10),
+                                   (5, 64, 1)])
+def test_route_topk(T, E, k):
+    rng = np.random.default_rng(T * 7 + E)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    if E == 512:  # config 5: +2 on 10% of experts
+        logits[:, rng.permutation(E)[: round(0.1 * E)]] += 2.0
+    idx, w = jq.moe_route(torch.from_numpy(logits).cuda(), k, renorm=True)
+    ridx, rw = O.route_topk(logits, k, renorm=True)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
+    _, w2 = jq.moe_route(torch.from_numpy(logits).cuda(), k, renorm=False)
+    np.testing.assert_allclose(w2.cpu().numpy(), O.route_topk(logits, k, renorm=False)[1],
+                               rtol=2e-6, atol=1e-8)
+
+
+def _stack(E, N, K, bits, gs, seed):
+    return QWeight(N, K, bits, gs, seed=seed, experts=E)
+
+
+@pytest.mark.parametrize("bits,gs", [(2, 64), (4, 32), (3, 128), (8, 64)])
+@pytest.mark.parametrize("M", [1, 3])
+def test_gather_qmm_pairs(bits, gs, M):
+    E, N, K = 8, 128, 256
+    qw = _stack(E, N, K, bits, gs, seed=bits + gs)
+    rng = np.random.default_rng(5)
+    B = 6
+    x = O.round_bf16(rng.standard_normal((B, M, K), dtype=np.float32))
+    lhs = np.array([0, 5, 5, 2, 3, 1, 0, 4, 2, 2], np.int32)
+    rhs = np.array([7, 0, 3, 3, 3, 1, 7, 6, 0, 3], np.int32)
+    y = jq.gather_qmm(to_tensor(x, "bf16"), qw.dw, qw.ds, qw.db,
+                      torch.from_numpy(lhs).cuda(), torch.from_numpy(rhs).cuda(),
+                      group_size=gs, bits=bits)
+    ref = O.gather_qmm(x, qw.packed, qw.s, qw.b, lhs, rhs, bits, gs)
+    assert tuple(y.shape) == (len(lhs), M, N)
+    assert_close(values_of(y), O.round_bf16(ref), f"gather b{bits} g{gs} M{M}")
+
+
+def test_gather_qmm_mlx_broadcasting_and_sorted_flag():
+    """SwitchGLU call shape: x [T,1,1,K], rhs [T,k] -> out [T,k,1,N]; the sorted path
+    (_gather_sort: rows permuted by expert, sorted_indices=True) gives the same rows."""
+    E, N, K, T, k = 16, 64, 128, 20, 4
+    qw = _stack(E, N, K, 4, 64, seed=9)
+    rng = np.random.default_rng(9)
+    x = O.round_bf16(rng.standard_normal((T, K), dtype=np.float32))
+    inds = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    tx = to_tensor(x, "bf16")
+    y = jq.gather_qmm(tx.reshape(T, 1, 1, K), qw.dw, qw.ds, qw.db,
+                      rhs_indices=torch.from_numpy(inds).cuda(), group_size=64, bits=4)
+    assert tuple(y.shape) == (T, k, 1, N)
+    ref = O.gather_qmm(x[:, None, :], qw.packed, qw.s, qw.b, np.repeat(np.arange(T), k),
+                       inds.reshape(-1), 4, 64)
+    assert_close(values_of(y).reshape(T * k, N), O.round_bf16(ref[:, 0]), "broadcast gather")
+    flat = inds.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    ys = jq.gather_qmm(tx[torch.from_numpy(order // k).cuda()].reshape(T * k, 1, K), qw.dw, qw.ds,
+                       qw.db, rhs_indices=torch.from_numpy(flat[order]).cuda(), group_size=64,
+                       bits=4, sorted_indices=True)
+    inv = np.argsort(order)
+    assert torch.equal(ys[torch.from_numpy(inv).cuda()].reshape(T, k, 1, N), y)
+
+
+@pytest.mark.parametrize("T,k,E,bits_gu,bits_d", [(1, 4, 32, 2, 2), (16, 4, 32, 2, 2),
+                                                  (64, 4, 32, 3, 4), (7, 2, 8, 8, 6)])
+def test_switch_glu(T, k, E, bits_gu, bits_d):
+    H, I, gs = 256, 128, 64
+    g = _stack(E, I, H, bits_gu, gs, seed=1)
+    u = _stack(E, I, H, bits_gu, gs, seed=2)
+    d = _stack(E, H, I, bits_d, gs, seed=3)
+    rng = np.random.default_rng(T)
+    x = O.round_bf16(rng.standard_normal((T, H), dtype=np.float32))
+    inds = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    out = jq.switch_glu(to_tensor(x, "bf16"), torch.from_numpy(inds).cuda(),
+                        (g.dw, g.ds, g.db, bits_gu), (u.dw, u.ds, u.db, bits_gu),
+                        (d.dw, d.ds, d.db, bits_d), gs)
+    ref, _ = O.switch_glu(x, inds, (g.packed, g.s, g.b, bits_gu), (u.packed, u.s, u.b, bits_gu),
+                          (d.packed, d.s, d.b, bits_d), gs, "bf16")
+    assert tuple(out.shape) == (T, k, H)
+    assert_close(values_of(out), ref, f"switch_glu T{T} k{k}")
+
+
+def test_moe_block_module():
+    """Router (8-bit gate) -> top-k -> SwitchGLU -> weighted sum + shared expert."""
+    H, I, E, k, T = 256, 128, 16, 4, 5
+    blk = jnn.SparseMoeBlock(H, I, E, k, shared_hidden=256, bits=2, device="cuda")
+    rng = np.random.default_rng(0)
+    ws = {}
+
+    def fill(lin, rows, K, bits, seed, experts=None):
+        q = QWeight(rows, K, bits, 64, seed=seed, experts=experts)
+        lin.weight, lin.scales, lin.biases = q.dw, q.ds, q.db
+        ws[id(lin)] = q
+        return q
+
+    gq = fill(blk.gate, E, H, 8, 10)
+    sg = [fill(blk.switch_mlp.gate_proj, I, H, 2, 11, E), fill(blk.switch_mlp.up_proj, I, H, 2, 12, E),
+          fill(blk.switch_mlp.down_proj, H, I, 2, 13, E)]
+    sh = [fill(blk.shared_expert.gate_proj, 256, H, 8, 14), fill(blk.shared_expert.up_proj, 256, H, 8, 15),
+          fill(blk.shared_expert.down_proj, H, 256, 8, 16)]
+    x = O.round_bf16(rng.standard_normal((T, H), dtype=np.float32))
+    y = blk(to_tensor(x, "bf16"))
+    logits = O.round_bf16(O.quantized_matmul(x, gq.packed, gq.s, gq.b, 8, 64))
+    idx, sc = O.route_topk(logits, k)
+    sw, _ = O.switch_glu(x, idx, *[(q.packed, q.s, q.b, 2) for q in sg], 64, "bf16")
+    routed = O.round_bf16((sw.astype(np.float64) * sc[..., None]).sum(1))
+    g = O.round_bf16(O.quantized_matmul(x, sh[0].packed, sh[0].s, sh[0].b, 8, 64))
+    u = O.round_bf16(O.quantized_matmul(x, sh[1].packed, sh[1].s, sh[1].b, 8, 64))
+    h = O.round_bf16(O.silu(g) * u)
+    shared = O.round_bf16(O.quantized_matmul(h, sh[2].packed, sh[2].s, sh[2].b, 8, 64))
+    assert_close(values_of(y), O.round_bf16(routed + shared), "moe block")

@@ -1,0 +1,317 @@
+"""Pins the CPU oracle (oracle/jangq_oracle.py, oracle/jq_oracle.c) before it is trusted as
+the checker of the GPU kernels. CPU only.
+
+Sources of truth, in order:
+  * known answers of the reference's own tests (jang-tools/tests/test_pack.py:33-61) and
+    their round-trip recipes (seeds 42 / 123 / 999, test_pack.py:11-22,63-87);
+  * the MLX-produced fixture jang-runtime/Tests/JANGCoreMetalTests/fixtures/
+    matmul_4bit_64x128.safetensors, regenerated from its recorded seed
+    (jang-tools/scripts/gen_matmul_fixture.py:33-46);
+  * closed forms and brute force (Python big-int bit streams, pure-Python loops);
+  * agreement of two independent restatements (numpy vs bit-by-bit C).
+Planted-mistake checks show each pin would catch a plausible error.
+"""
+import ctypes
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import jangq_oracle as O
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def _bigint_stream(values, bits):
+    """LSB-first definition with Python integers: value i at bit i*bits."""
+    acc = 0
+    for i, v in enumerate(values):
+        acc |= int(v) << (i * bits)
+    nbytes = (len(values) * bits + 7) // 8
+    return list(acc.to_bytes(nbytes, "little"))
+
+
+# ----------------------------------------------------------------------------- packing
+
+
+def test_pack_known_answers_from_reference_tests():
+    # jang-tools/tests/test_pack.py:33-44 (2-bit), :46-52 (1-bit), :54-61 (4-bit)
+    assert O.pack_bits([0, 1, 2, 3, 0, 1, 2, 3], 2).tolist() == [0xE4, 0xE4]
+    assert O.pack_bits([0, 1, 0, 1, 1, 0, 1, 0], 1).tolist() == [0b01011010]
+    assert O.pack_bits([5, 10, 3, 15], 4).tolist() == [0xA5, 0xF3]
+    np.testing.assert_array_equal(O.unpack_bits(np.array([0xE4, 0xE4], np.uint8), 2, 8),
+                                  [0, 1, 2, 3, 0, 1, 2, 3])
+
+
+def test_pack_word_straddling_vectors():
+    # 3-bit: codes 2 and 5 cross byte boundaries; LSB-first value 0x8B03DD.
+    assert O.pack_bits([5, 3, 7, 1, 0, 6, 2, 4], 3).tolist() == [0xDD, 0x03, 0x8B]
+    # 6-bit: 63 | 42<<12 | 21<<18 = 0x56A03F.
+    assert O.pack_bits([63, 0, 42, 21], 6).tolist() == [0x3F, 0xA0, 0x56]
+    # Codes crossing uint32 words in a 3/5/6-bit row agree with the big-int definition.
+    rng = np.random.default_rng(7)
+    for bits in (3, 5, 6):
+        vals = rng.integers(0, 1 << bits, size=96)
+        assert O.pack_bits(vals, bits).tolist() == _bigint_stream(vals, bits)
+
+
+def test_known_answers_catch_msb_first_packing():
+    """Planted mistake: an MSB-first packer fails the reference known answers."""
+    def msb_first(values, bits):
+        v = np.asarray(values, np.uint64)
+        planes = ((v[:, None] >> np.arange(bits - 1, -1, -1, dtype=np.uint64)) & 1).astype(np.uint8)
+        return np.packbits(planes.reshape(-1), bitorder="big")
+    assert msb_first([5, 10, 3, 15], 4).tolist() != [0xA5, 0xF3]
+    assert msb_first([5, 3, 7, 1, 0, 6, 2, 4], 3).tolist() != [0xDD, 0x03, 0x8B]
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("seed,n", [(42, 64), (123, 64), (999, 6400)])
+def test_roundtrip_reference_recipes(bits, seed, n):
+    # test_pack.py:11-22 / 63-74 / 76-87
+    rng = np.random.default_rng(seed)
+    values = rng.integers(0, (1 << bits), size=n, dtype=np.uint8)
+    packed = O.pack_bits(values, bits)
+    assert len(packed) == (n * bits + 7) // 8  # test_pack.py:24-31
+    np.testing.assert_array_equal(O.unpack_bits(packed, bits, n), values)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 8])
+def test_max_and_zero_values(bits):
+    for fill in (0, (1 << bits) - 1):  # test_pack.py:89-104
+        v = np.full(64, fill, dtype=np.uint8)
+        np.testing.assert_array_equal(O.unpack_bits(O.pack_bits(v, bits), bits, 64), v)
+
+
+def test_unpack_flattens_packed_matrix_view():
+    values = np.array([0, 1] * 32, dtype=np.uint8)  # test_pack.py:106-110
+    np.testing.assert_array_equal(O.unpack_bits(O.pack_bits(values, 1).reshape(2, 4), 1, 64), values)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+def test_numpy_and_bitwise_c_restatements_agree(bits, c_oracle):
+    rng = np.random.default_rng(100 + bits)
+    rows, K = 7, 256
+    codes = rng.integers(0, 1 << bits, size=(rows, K), dtype=np.uint8)
+    packed = O.pack_rows(codes, bits)
+    w_c = np.zeros_like(packed)
+    c_oracle.jqo_pack(codes.ctypes.data, bits, rows, K, w_c.ctypes.data)
+    np.testing.assert_array_equal(w_c, packed)
+    out = np.zeros((rows, K), np.uint8)
+    c_oracle.jqo_unpack(packed.ctypes.data, bits, rows, K, out.ctypes.data)
+    np.testing.assert_array_equal(out, codes)
+    np.testing.assert_array_equal(O.unpack_rows(packed, bits), codes)
+
+
+# ----------------------------------------------------------------------------- MLX fixture
+
+
+def _fixture():
+    from safetensors.numpy import load_file
+
+    d = load_file(str(GOLD / "matmul_4bit_64x128.safetensors"))
+    info = json.loads((GOLD / "fixture_info.json").read_text())
+    rng = np.random.default_rng(info["seed"])  # gen_matmul_fixture.py:33-35
+    W = rng.standard_normal((info["out_features"], info["in_features"])).astype(np.float32)
+    x = rng.standard_normal((info["in_features"],)).astype(np.float16)
+    return d, info, W, x
+
+
+def test_fixture_inputs_regenerate_from_seed():
+    d, info, W, x = _fixture()
+    np.testing.assert_array_equal(x, d["x"])
+    assert info["bits"] == 4 and info["group_size"] == 64
+
+
+def test_quantizer_reproduces_mlx_codes_and_sidecars():
+    """mx.quantize output stored by the reference: codes and f16-cast sidecars bit-equal."""
+    d, info, W, _ = _fixture()
+    packed, s, b, _ = O.quantize_affine(W, info["bits"], info["group_size"], sidecar="f32")
+    np.testing.assert_array_equal(packed, d["W.weight"])
+    np.testing.assert_array_equal(s.astype(np.float16), d["W.scales"])
+    np.testing.assert_array_equal(b.astype(np.float16), d["W.biases"])
+
+
+def test_dequant_matmul_reproduces_mlx_y_ref():
+    """y_ref = mx.dequantize(q, s, b) @ x with MLX's fp32 sidecars (gen_matmul_fixture.py:44-46)."""
+    d, info, W, x = _fixture()
+    packed, s, b, _ = O.quantize_affine(W, 4, 64, sidecar="f32")
+    y = O.quantized_matmul(x.astype(np.float32)[None], packed, s, b, 4, 64)[0]
+    assert O.rel_l2(y, d["y_ref"]) < 1e-6
+    assert O.max_abs(y, d["y_ref"]) < 1e-4
+    # With the stored f16 sidecars: the reference's own acceptance bound (1e-2,
+    # QuantizedMatmul4Tests.swift:83-84).
+    y16 = O.quantized_matmul(x.astype(np.float32)[None], d["W.weight"],
+                             d["W.scales"].astype(np.float32), d["W.biases"].astype(np.float32),
+                             4, 64)[0]
+    assert O.max_abs(y16, d["y_ref"]) < 1e-2
+
+
+def test_fixture_catches_wrong_sign_convention():
+    """Planted mistake: always-positive scale (bias = min) gives different codes."""
+    d, info, W, _ = _fixture()
+    g = W.reshape(128, 1, 64)
+    lo, hi = g.min(-1), np.maximum(g.max(-1), 0)
+    s = (hi - lo) / 15
+    codes = np.clip(np.rint((g - lo[..., None]) / s[..., None]), 0, 15).astype(np.uint8)
+    assert not np.array_equal(O.pack_rows(codes.reshape(128, 64), 4), d["W.weight"])
+
+
+# ----------------------------------------------------------------------------- dequant
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+def test_dequant_identity_scale_returns_codes(bits):
+    # jang_tools/jangh/tests/test_jangtq2.py:19-24: dequantize(s=1, b=0) == q
+    rng = np.random.default_rng(bits)
+    codes = rng.integers(0, 1 << bits, size=(4, 128), dtype=np.uint8)
+    packed = O.pack_rows(codes, bits)
+    ones = np.ones((4, 2), np.float32)
+    np.testing.assert_array_equal(O.dequantize_affine(packed, ones, 0 * ones, bits, 64), codes)
+
+
+def test_dequant_rounds_product_and_sum_separately(c_oracle):
+    """fl(fl(q*s)+b) (numpy's q*s + b, affine.py:458-463) differs from a fused FMA on some
+    elements; the oracle and the C restatement agree with the two-rounding form."""
+    rng = np.random.default_rng(5)
+    rows, K, gs = 64, 256, 64
+    codes = rng.integers(0, 16, size=(rows, K), dtype=np.uint8)
+    packed = O.pack_rows(codes, 4)
+    s = rng.standard_normal((rows, K // gs)).astype(np.float32) * np.float32(0.013)
+    b = rng.standard_normal((rows, K // gs)).astype(np.float32) * np.float32(0.07)
+    deq = O.dequantize_affine(packed, s, b, 4, gs)
+    q = codes.astype(np.float32).reshape(rows, -1, gs)
+    two = (np.float32(1) * (q * s[..., None]).astype(np.float32) + b[..., None]).reshape(rows, K)
+    fused = (q.astype(np.float64) * s[..., None] + b[..., None]).astype(np.float32).reshape(rows, K)
+    np.testing.assert_array_equal(deq, two)
+    assert (fused != two).any(), "test inputs do not discriminate fused from two roundings"
+    out = np.zeros((rows, K), np.float32)
+    c_oracle.jqo_dequant(packed.ctypes.data, s.ctypes.data, b.ctypes.data, 4, gs, rows, K,
+                         out.ctypes.data)
+    np.testing.assert_array_equal(out, deq)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 6, 8])
+def test_dequant_stacked_experts_flatten(bits):
+    rng = np.random.default_rng(11)
+    w = O.round_bf16(rng.standard_normal((3 * 8, 128)).astype(np.float32) * 0.02)
+    packed, s, b, _ = O.quantize_affine(w, bits, 32)
+    flat = O.dequantize_affine(packed, O.sidecar_f32(s, "bf16"), O.sidecar_f32(b, "bf16"), bits, 32)
+    stacked = O.dequantize_affine(packed.reshape(3, 8, -1), O.sidecar_f32(s, "bf16").reshape(3, 8, -1),
+                                  O.sidecar_f32(b, "bf16").reshape(3, 8, -1), bits, 32)
+    np.testing.assert_array_equal(stacked.reshape(24, 128), flat)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_quantizer_invariants(bits, gs):
+    rng = np.random.default_rng(bits * 1000 + gs)
+    w = O.round_bf16(rng.standard_normal((16, 256)).astype(np.float32) * 0.02)
+    packed, s, b, codes = O.quantize_affine(w, bits, gs, sidecar="f32")
+    assert codes.max() <= (1 << bits) - 1
+    np.testing.assert_array_equal(O.unpack_rows(packed, bits), codes)
+    deq = O.dequantize_affine(packed, s, b, bits, gs).reshape(16, -1, gs)
+    err = np.abs(deq - w.reshape(16, -1, gs))
+    # unclipped codes reconstruct within half a step; the refined scale may clip the
+    # non-dominant edge to 2^b - 1 (affine.py:240-252)
+    unclipped = codes.reshape(16, -1, gs) < (1 << bits) - 1
+    bound = np.abs(s)[..., None] * 0.5 * (1 + 1e-5) + 1e-7
+    assert np.all((err <= bound) | ~unclipped)
+    # the dominant edge is hit exactly by code 0 (bias = edge)
+    g = w.reshape(16, -1, gs)
+    edge_idx = np.where(np.abs(g.min(-1)) > np.abs(np.maximum(g.max(-1), 0)),
+                        g.argmin(-1), g.argmax(-1))
+    edge_codes = np.take_along_axis(codes.reshape(16, -1, gs), edge_idx[..., None], -1)[..., 0]
+    assert np.all(edge_codes == 0)
+
+
+def test_f16_sidecar_guard():
+    # affine.py:43-51: a zero / sub-f16 scale is stored as +-2^-14, never 0.
+    w = np.zeros((1, 64), np.float32)
+    _, s, _, _ = O.quantize_affine(w, 4, 64, sidecar="f16")
+    assert s.dtype == np.float16 and s[0, 0] != 0
+    assert abs(float(s[0, 0])) == float(np.finfo(np.float16).smallest_normal)
+
+
+# ----------------------------------------------------------------------------- matmuls
+
+
+def test_quantized_matmul_vs_pure_python_loop():
+    rng = np.random.default_rng(3)
+    w = O.round_bf16(rng.standard_normal((3, 64)).astype(np.float32) * 0.02)
+    packed, s, b, codes = O.quantize_affine(w, 3, 32)
+    sf, bf = O.sidecar_f32(s, "bf16"), O.sidecar_f32(b, "bf16")
+    x = O.round_bf16(rng.standard_normal((2, 64)).astype(np.float32))
+    y = O.quantized_matmul(x, packed, sf, bf, 3, 32)
+    for m in range(2):
+        for n in range(3):
+            acc = 0.0
+            for k in range(64):
+                wq = np.float32(np.float32(codes[n, k]) * sf[n, k // 32]) + bf[n, k // 32]
+                acc += float(x[m, k]) * float(np.float32(wq))
+            assert abs(acc - y[m, n]) < 1e-12
+
+
+def test_c_gemm_matches_numpy(c_oracle):
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((3, 96)).astype(np.float32)
+    W = rng.standard_normal((5, 96)).astype(np.float32)
+    y = np.zeros((3, 5), np.float64)
+    c_oracle.jqo_gemm_f64(x.ctypes.data, W.ctypes.data, 3, 5, 96, y.ctypes.data)
+    np.testing.assert_allclose(y, x.astype(np.float64) @ W.T.astype(np.float64), rtol=1e-12)
+
+
+def test_gather_qmm_vs_loop_and_dense():
+    rng = np.random.default_rng(9)
+    E, N, K = 4, 8, 64
+    w = O.round_bf16(rng.standard_normal((E * N, K)).astype(np.float32) * 0.02)
+    packed, s, b, _ = O.quantize_affine(w, 4, 32)
+    P = packed.reshape(E, N, -1)
+    sf = O.sidecar_f32(s, "bf16").reshape(E, N, -1)
+    bf = O.sidecar_f32(b, "bf16").reshape(E, N, -1)
+    x = O.round_bf16(rng.standard_normal((5, 1, K)).astype(np.float32))
+    lhs = np.array([0, 1, 1, 4, 2, 3])
+    rhs = np.array([3, 0, 2, 2, 1, 0])
+    out = O.gather_qmm(x, P, sf, bf, lhs, rhs, 4, 32)
+    for i in range(len(lhs)):
+        ref = O.quantized_matmul(x[lhs[i]], P[rhs[i]], sf[rhs[i]], bf[rhs[i]], 4, 32)
+        np.testing.assert_array_equal(out[i], ref)
+
+
+def test_switch_glu_equals_composed_gathers():
+    """SwitchGLU = gather(gate), gather(up), silu*up, gather(down) (dots3/ops.py:215-223)."""
+    rng = np.random.default_rng(12)
+    E, H, I, T, k = 4, 64, 32, 3, 2
+
+    def stack(rows, K, bits, seed):
+        r = np.random.default_rng(seed)
+        w = O.round_bf16(r.standard_normal((E * rows, K)).astype(np.float32) * 0.02)
+        p, s, b, _ = O.quantize_affine(w, bits, 32)
+        return (p.reshape(E, rows, -1), O.sidecar_f32(s, "bf16").reshape(E, rows, -1),
+                O.sidecar_f32(b, "bf16").reshape(E, rows, -1), bits)
+
+    g, u, d = stack(I, H, 4, 1), stack(I, H, 4, 2), stack(H, I, 2, 3)
+    x = O.round_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    idx = np.array([[0, 3], [2, 0], [1, 1]])
+    out, _ = O.switch_glu(x, idx, g, u, d, 32, "bf16")
+    lhs = np.repeat(np.arange(T), k)
+    gg = O.round_bf16(O.gather_qmm(x[:, None, :], *g[:3], lhs, idx.reshape(-1), 4, 32))
+    uu = O.round_bf16(O.gather_qmm(x[:, None, :], *u[:3], lhs, idx.reshape(-1), 4, 32))
+    h = O.round_bf16(O.silu(gg) * uu)
+    dd = O.round_bf16(O.gather_qmm(h, *d[:3], np.arange(T * k), idx.reshape(-1), 2, 32))
+    np.testing.assert_array_equal(out.reshape(T * k, H), dd[:, 0, :])
+
+
+def test_route_topk_vs_full_sort():
+    rng = np.random.default_rng(13)
+    logits = rng.standard_normal((6, 32)).astype(np.float32)
+    logits[0, 5] = logits[0, 9] = 9.0  # exact tie: lower id first
+    idx, w = O.route_topk(logits, 4, renorm=True)
+    for t in range(6):
+        p = np.exp(logits[t].astype(np.float64) - logits[t].max())
+        p /= p.sum()
+        order = sorted(range(32), key=lambda e: (-p[e], e))[:4]
+        assert idx[t].tolist() == order
+        np.testing.assert_allclose(w[t], p[order] / p[order].sum(), rtol=1e-12)
+    assert idx[0, 0] == 5 and idx[0, 1] == 9
