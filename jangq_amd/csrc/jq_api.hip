@@ -9,6 +9,14 @@ int dense_one(const void* x, int xd, const uint32_t* codes, const void* scales,
               const void* biases, int sb, int bits, int gs, int64_t M, int64_t N, int64_t K,
               void* y, int yd, hipStream_t st) {
   const bool mfma_ok = (xd == JQ_BF16 || xd == JQ_F16) && K % 128 == 0;
+  if (jqk::dec_dense_ok((int)(M < (1 << 30) ? M : (1 << 30)), K, gs, xd, sb)) {
+    jqk::QmvBatch b;
+    b.M = (int)M;
+    b.K = (int)K;
+    b.p[0].x = x; b.p[0].codes = codes; b.p[0].scales = scales; b.p[0].biases = biases;
+    b.p[0].y = y; b.p[0].N = N;
+    return jqk::dec_dense_launch(b, 1, bits, gs, xd, sb, yd, st);
+  }
   if (M > 4 && mfma_ok) {
     jqk::QmmProblem p;
     p.x = x; p.codes = codes; p.scales = scales; p.biases = biases; p.y = y;
@@ -95,7 +103,9 @@ int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
   bool same = count <= jqk::kMaxProblems;
   for (int i = 1; i < count && same; ++i)
     same = bits[i] == bits[0] && group_size[i] == group_size[0] && M[i] == M[0] && K[i] == K[0];
-  if (same && M[0] >= 1 && M[0] <= 4 && K[0] > 0) {
+  const bool dec = same && jqk::dec_dense_ok((int)(M[0] < (1 << 30) ? M[0] : (1 << 30)), K[0],
+                                             group_size[0], x_dtype, sb_dtype);
+  if (dec || (same && M[0] >= 1 && M[0] <= 4 && K[0] > 0)) {
     jqk::QmvBatch b;
     b.M = (int)M[0];
     b.K = (int)K[0];
@@ -110,6 +120,7 @@ int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
       b.p[n].N = N[i];
       ++n;
     }
+    if (dec) return jqk::dec_dense_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
     return jqk::qmv_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
   }
   for (int i = 0; i < count; ++i) {

@@ -88,6 +88,35 @@ JQ_DEV uint32_t unit_code_rt(const uint32_t* w, int i) {
   return (uint32_t)(two >> sh) & ((1u << BITS) - 1u);
 }
 
+// One 32-code unit (BITS words) in registers, loaded with the widest aligned vector loads.
+template <int BITS>
+struct UnitWords {
+  uint32_t w[BITS];
+};
+
+template <int BITS>
+JQ_DEV UnitWords<BITS> load_unit(const uint32_t* __restrict__ p) {
+  UnitWords<BITS> u;
+  if constexpr (BITS == 4) {
+    const uint4 v = *(const uint4*)p;
+    u.w[0] = v.x; u.w[1] = v.y; u.w[2] = v.z; u.w[3] = v.w;
+  } else if constexpr (BITS == 2) {
+    const uint2 v = *(const uint2*)p;
+    u.w[0] = v.x; u.w[1] = v.y;
+  } else if constexpr (BITS == 8) {
+    const uint4 a = *(const uint4*)p, b = *(const uint4*)(p + 4);
+    u.w[0] = a.x; u.w[1] = a.y; u.w[2] = a.z; u.w[3] = a.w;
+    u.w[4] = b.x; u.w[5] = b.y; u.w[6] = b.z; u.w[7] = b.w;
+  } else if constexpr (BITS == 6) {
+    const uint2 a = *(const uint2*)p, b = *(const uint2*)(p + 2), c = *(const uint2*)(p + 4);
+    u.w[0] = a.x; u.w[1] = a.y; u.w[2] = b.x; u.w[3] = b.y; u.w[4] = c.x; u.w[5] = c.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < BITS; ++i) u.w[i] = p[i];
+  }
+  return u;
+}
+
 // ----------------------------------------------------------------------------- magic pairs
 //
 // The matmul kernels never convert codes with int->float instructions. For an 8-code chunk
@@ -183,6 +212,23 @@ JQ_DEV void pair_activations(const uint32_t d[4], uint32_t out[4]) {
   out[1] = __builtin_amdgcn_perm(d[2], d[0], 0x07060302u);
   out[2] = __builtin_amdgcn_perm(d[3], d[1], 0x05040100u);
   out[3] = __builtin_amdgcn_perm(d[3], d[1], 0x07060302u);
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// D = A(16x32) * B(32x16) + C with 16-bit float operands of format FMT (v_mfma_f32_16x16x32).
+template <int FMT>
+JQ_DEV f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (FMT == JQ_BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
 }
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;

@@ -15,8 +15,10 @@ namespace {
 
 using namespace jq;
 
-// Rows per tile of the grouped matrix-core kernel (must match qmm_gather_launch).
-constexpr int kTileRows = 16;
+// Rows per tile of the grouped kernels: 16 for the LDS-staged GEMM, 16/8/4 (gs 128/64/32)
+// for the decode kernel. Workspaces are sized for the smallest tile.
+constexpr int kMinTileRows = 4;
+constexpr int kGemmTileRows = 16;
 constexpr int kMaxExperts = 4096;
 
 // One wave per token. Lanes hold E/64 logits each; top-k by k rounds of wave argmax
@@ -101,12 +103,12 @@ JQ_DEV int block_exclusive_scan(int v, int* sh_wave, int& total) {
 //   seg_off[E+1]  exclusive offsets of each expert's segment in `order`
 //   order         pair ids grouped by expert (order inside a segment is arbitrary: it does
 //                 not change any value). Pairs whose expert id is >= E are left out.
-//   tiles         (expert, first row, rows) for every kTileRows-row tile of every segment
+//   tiles         (expert, first row, rows) for every tile_rows-row tile of every segment
 //                 (segment rows = count * M)
 //   n_tiles[0]    number of tiles
 __global__ void __launch_bounds__(1024) plan_kernel(const uint32_t* __restrict__ rhs, int n_pairs,
-                                                    int E, int M, int* seg_off, uint32_t* order,
-                                                    int4* tiles, int* n_tiles) {
+                                                    int E, int M, int tile_rows, int* seg_off,
+                                                    uint32_t* order, int4* tiles, int* n_tiles) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int cur[kMaxExperts];
   __shared__ int sh_wave[40];
@@ -124,7 +126,7 @@ __global__ void __launch_bounds__(1024) plan_kernel(const uint32_t* __restrict__
   int local = 0, ltiles = 0;
   for (int e = e0; e < e0 + per && e < E; ++e) {
     local += cnt[e];
-    ltiles += (cnt[e] * M + kTileRows - 1) / kTileRows;
+    ltiles += (cnt[e] * M + tile_rows - 1) / tile_rows;
   }
   int total;
   int base = block_exclusive_scan(local, sh_wave, total);
@@ -134,8 +136,8 @@ __global__ void __launch_bounds__(1024) plan_kernel(const uint32_t* __restrict__
     seg_off[e] = base;
     cur[e] = base;
     const int rows = cnt[e] * M;
-    for (int r = 0; r < rows; r += kTileRows) {
-      tiles[tbase++] = make_int4(e, r, rows - r < kTileRows ? rows - r : kTileRows, 0);
+    for (int r = 0; r < rows; r += tile_rows) {
+      tiles[tbase++] = make_int4(e, r, rows - r < tile_rows ? rows - r : tile_rows, 0);
     }
     base += cnt[e];
   }
@@ -156,9 +158,9 @@ struct WsLayout {
 
 inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
-inline int64_t max_tiles_for(int64_t n_pairs, int64_t E, int64_t M) {
+inline int64_t max_tiles_for(int64_t n_pairs, int64_t E, int64_t M, int tile_rows) {
   const int64_t active = n_pairs < E ? n_pairs : E;
-  return (n_pairs * M + kTileRows - 1) / kTileRows + active;
+  return (n_pairs * M + tile_rows - 1) / tile_rows + active;
 }
 
 inline WsLayout ws_layout(int64_t n_pairs, int64_t E, int64_t M) {
@@ -166,14 +168,14 @@ inline WsLayout ws_layout(int64_t n_pairs, int64_t E, int64_t M) {
   int64_t o = 0;
   L.seg_off = o; o = align256(o + (E + 1) * 4);
   L.order = o; o = align256(o + n_pairs * 4);
-  L.tiles = o; o = align256(o + max_tiles_for(n_pairs, E, M) * 16);
+  L.tiles = o; o = align256(o + max_tiles_for(n_pairs, E, M, kMinTileRows) * 16);
   L.n_tiles = o; o = align256(o + 4);
   L.total = o;
   return L;
 }
 
-int build_plan(const uint32_t* rhs, int64_t n_pairs, int64_t E, int64_t M, void* ws,
-               jqk::GatherPlan& plan, const uint32_t* lhs, hipStream_t st) {
+int build_plan(const uint32_t* rhs, int64_t n_pairs, int64_t E, int64_t M, int tile_rows,
+               void* ws, jqk::GatherPlan& plan, const uint32_t* lhs, hipStream_t st) {
   const WsLayout L = ws_layout(n_pairs, E, M);
   char* base = (char*)ws;
   plan.seg_off = (const int*)(base + L.seg_off);
@@ -184,10 +186,19 @@ int build_plan(const uint32_t* rhs, int64_t n_pairs, int64_t E, int64_t M, void*
   plan.M = (int)M;
   plan.pair_div = 1;
   plan.x_rows = 0;
-  plan_kernel<<<1, 1024, 0, st>>>(rhs, (int)n_pairs, (int)E, (int)M, (int*)(base + L.seg_off),
+  plan_kernel<<<1, 1024, 0, st>>>(rhs, (int)n_pairs, (int)E, (int)M, tile_rows,
+                                  (int*)(base + L.seg_off),
                                   (uint32_t*)(base + L.order), (int4*)(base + L.tiles),
                                   (int*)(base + L.n_tiles));
   return jqh::launch_status();
+}
+
+// Decode-sized grouped problems (few rows per selected expert) run on the streaming decode
+// kernel; larger ones on the LDS-staged GEMM with 16-row tiles.
+bool use_decode_kernel(int64_t rows, int64_t E, int64_t n_pairs, int gs, int xd, int sb) {
+  if (!((xd == JQ_BF16 || xd == JQ_F16) && (sb == JQ_BF16 || sb == JQ_F16))) return false;
+  const int64_t active = n_pairs < E ? n_pairs : E;
+  return rows <= 2 * active * jqk::dec_tokens_per_block(gs);
 }
 
 int check_expert_shape(int bits, int gs, int64_t E, int64_t N, int64_t K) {
@@ -235,7 +246,9 @@ int jq_gather_qmm(const void* x, int x_dtype, int64_t x_batch, int64_t M, const 
   hipStream_t st = (hipStream_t)stream;
   jqk::GatherPlan plan;
   (void)sorted_indices;  // grouping is done on the device in every case
-  s = build_plan(rhs, n_pairs, E, M, workspace, plan, lhs, st);
+  const bool dec = use_decode_kernel(n_pairs * M, E, n_pairs, group_size, x_dtype, sb_dtype);
+  const int tile_rows = dec ? jqk::dec_tokens_per_block(group_size) : kGemmTileRows;
+  s = build_plan(rhs, n_pairs, E, M, tile_rows, workspace, plan, lhs, st);
   if (s) return s;
   plan.x_rows = x_batch * M;
   jqk::QmmProblem p;
@@ -249,8 +262,11 @@ int jq_gather_qmm(const void* x, int x_dtype, int64_t x_batch, int64_t M, const 
   p.K = K;
   p.expert_stride_codes = N * (K * bits / 32);
   p.expert_stride_sb = N * (K / group_size);
-  return jqk::qmm_gather_launch(p, nullptr, plan, max_tiles_for(n_pairs, E, M), bits, group_size,
-                                x_dtype, sb_dtype, y_dtype, st);
+  const int64_t mt = max_tiles_for(n_pairs, E, M, tile_rows);
+  if (dec) return jqk::dec_gather_launch(p, nullptr, plan, mt, bits, group_size, x_dtype, sb_dtype,
+                                         y_dtype, st);
+  return jqk::qmm_gather_launch(p, nullptr, plan, mt, bits, group_size, x_dtype, sb_dtype,
+                                y_dtype, st);
 }
 
 int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E,
@@ -278,8 +294,10 @@ int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, i
   hipStream_t st = (hipStream_t)stream;
   // Pair i = t*k + j uses x row t = i / k and expert idx[i]; one plan serves both launches
   // (gate+up reads x rows i / k, down reads h rows i).
+  const bool dec = use_decode_kernel(n_pairs, E, n_pairs, group_size, x_dtype, sb_dtype);
+  const int tile_rows = dec ? jqk::dec_tokens_per_block(group_size) : kGemmTileRows;
   jqk::GatherPlan plan;
-  s = build_plan(idx, n_pairs, E, 1, workspace, plan, nullptr, st);
+  s = build_plan(idx, n_pairs, E, 1, tile_rows, workspace, plan, nullptr, st);
   if (s) return s;
   jqk::GatherPlan plan_gu = plan;
   plan_gu.lhs = nullptr;
@@ -293,14 +311,18 @@ int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, i
   g.expert_stride_sb = I * (H / group_size);
   u = g;
   u.codes = up_codes; u.scales = up_scales; u.biases = up_biases;
-  const int64_t mt = max_tiles_for(n_pairs, E, 1);
-  s = jqk::qmm_gather_launch(g, &u, plan_gu, mt, bits_gu, group_size, x_dtype, sb_dtype, y_dtype,
-                             st);
+  const int64_t mt = max_tiles_for(n_pairs, E, 1, tile_rows);
+  s = dec ? jqk::dec_gather_launch(g, &u, plan_gu, mt, bits_gu, group_size, x_dtype, sb_dtype,
+                                   y_dtype, st)
+          : jqk::qmm_gather_launch(g, &u, plan_gu, mt, bits_gu, group_size, x_dtype, sb_dtype,
+                                   y_dtype, st);
   if (s) return s;
   d.x = h_buf; d.codes = down_codes; d.scales = down_scales; d.biases = down_biases; d.y = out;
   d.M = 1; d.N = H; d.K = I;
   d.expert_stride_codes = H * (I * bits_d / 32);
   d.expert_stride_sb = H * (I / group_size);
+  if (dec) return jqk::dec_gather_launch(d, nullptr, plan, mt, bits_d, group_size, y_dtype,
+                                         sb_dtype, y_dtype, st);
   return jqk::qmm_gather_launch(d, nullptr, plan, mt, bits_d, group_size, y_dtype, sb_dtype,
                                 y_dtype, st);
 }

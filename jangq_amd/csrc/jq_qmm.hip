@@ -29,22 +29,6 @@ using namespace jq;
 using jqk::GatherPlan;
 using jqk::QmmProblem;
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-template <int FMT>
-JQ_DEV f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
-  if constexpr (FMT == JQ_BF16) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-}
-
 constexpr int KT = 128;  // codes per k-tile
 
 template <int BITS_, int GS_, int BM_, int BN_, int WGM_, int WGN_, int XDT_, int NB_ = 1>

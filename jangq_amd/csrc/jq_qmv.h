@@ -64,4 +64,14 @@ int qmm_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPla
                       int64_t max_tiles, int bits, int gs, int xd, int sb, int yd,
                       hipStream_t st);
 
+// Decode-shaped matrix-core kernels (jq_dec.hip): activation rows per MFMA block for a
+// group size, eligibility of a dense problem, dense and grouped launches.
+int dec_tokens_per_block(int gs);
+bool dec_dense_ok(int M, int64_t K, int gs, int xd, int sb);
+int dec_dense_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
+                     hipStream_t st);
+int dec_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPlan& plan,
+                      int64_t max_tiles, int bits, int gs, int xd, int sb, int yd,
+                      hipStream_t st);
+
 }  // namespace jqk

@@ -24,34 +24,6 @@ using jqk::QmvProblem;
 
 constexpr int kWaves = 4;  // waves per block
 
-template <int BITS>
-struct UnitWords {
-  uint32_t w[BITS];
-};
-
-template <int BITS>
-JQ_DEV UnitWords<BITS> load_unit(const uint32_t* __restrict__ p) {
-  UnitWords<BITS> u;
-  if constexpr (BITS == 4) {
-    const uint4 v = *(const uint4*)p;
-    u.w[0] = v.x; u.w[1] = v.y; u.w[2] = v.z; u.w[3] = v.w;
-  } else if constexpr (BITS == 2) {
-    const uint2 v = *(const uint2*)p;
-    u.w[0] = v.x; u.w[1] = v.y;
-  } else if constexpr (BITS == 8) {
-    const uint4 a = *(const uint4*)p, b = *(const uint4*)(p + 4);
-    u.w[0] = a.x; u.w[1] = a.y; u.w[2] = a.z; u.w[3] = a.w;
-    u.w[4] = b.x; u.w[5] = b.y; u.w[6] = b.z; u.w[7] = b.w;
-  } else if constexpr (BITS == 6) {
-    const uint2 a = *(const uint2*)p, b = *(const uint2*)(p + 2), c = *(const uint2*)(p + 4);
-    u.w[0] = a.x; u.w[1] = a.y; u.w[2] = b.x; u.w[3] = b.y; u.w[4] = c.x; u.w[5] = c.y;
-  } else {
-#pragma unroll
-    for (int i = 0; i < BITS; ++i) u.w[i] = p[i];
-  }
-  return u;
-}
-
 // Activations of one unit for one token: 32 values as 16 paired dwords plus their fp32 sum.
 template <int XDT>
 struct XUnit {

@@ -42,6 +42,16 @@ def test_matmul_bits_groups(bits, gs, M):
     run_case(M, 96, 512, bits, gs, seed=bits * 10 + gs + M)
 
 
+@pytest.mark.parametrize("gs,tpb", [(32, 4), (64, 8), (128, 16)])
+@pytest.mark.parametrize("bits", [2, 3, 4, 6, 8])
+def test_decode_kernel_token_limits(gs, tpb, bits):
+    """Largest batch on the decode matrix-core kernel (tokens per block = 16 / (128/gs)) and
+    one more (next kernel), bf16 and f16 activations."""
+    for M in (1, tpb, tpb + 1):
+        run_case(M, 48, 384, bits, gs, seed=M * 31 + bits)
+        run_case(M, 40, 256, bits, gs, xdt="f16", sidecar="f16", seed=M * 37 + bits)
+
+
 @pytest.mark.parametrize("M", [1, 2, 4, 5, 16, 17, 64, 130])
 def test_matmul_m_sweep_fp32_out(M):
     run_case(M, 200, 1024, 4, 64, seed=M, ydt="f32")

@@ -50,6 +50,21 @@ def test_gather_qmm_pairs(bits, gs, M):
     assert_close(values_of(y), O.round_bf16(ref), f"gather b{bits} g{gs} M{M}")
 
 
+@pytest.mark.parametrize("bits,gs", [(2, 64), (4, 128)])
+def test_gather_qmm_many_rows_per_expert(bits, gs):
+    """Prefill-like grouping (hundreds of rows over 4 experts) takes the 16-row-tile GEMM."""
+    E, N, K, n = 4, 96, 256, 300
+    qw = _stack(E, N, K, bits, gs, seed=21)
+    rng = np.random.default_rng(21)
+    x = O.round_bf16(rng.standard_normal((n, 1, K), dtype=np.float32))
+    rhs = rng.integers(0, E, size=n).astype(np.int32)
+    rhs[:7] = 3  # skew
+    y = jq.gather_qmm(to_tensor(x, "bf16"), qw.dw, qw.ds, qw.db,
+                      rhs_indices=torch.from_numpy(rhs).cuda(), group_size=gs, bits=bits)
+    ref = O.gather_qmm(x, qw.packed, qw.s, qw.b, np.arange(n), rhs, bits, gs)
+    assert_close(values_of(y), O.round_bf16(ref), "many rows per expert")
+
+
 def test_gather_qmm_mlx_broadcasting_and_sorted_flag():
     """SwitchGLU call shape: x [T,1,1,K], rhs [T,k] -> out [T,k,1,N]; the sorted path
     (_gather_sort: rows permuted by expert, sorted_indices=True) gives the same rows."""
@@ -75,7 +90,8 @@ def test_gather_qmm_mlx_broadcasting_and_sorted_flag():
 
 
 @pytest.mark.parametrize("T,k,E,bits_gu,bits_d", [(1, 4, 32, 2, 2), (16, 4, 32, 2, 2),
-                                                  (64, 4, 32, 3, 4), (7, 2, 8, 8, 6)])
+                                                  (64, 4, 32, 3, 4), (7, 2, 8, 8, 6),
+                                                  (160, 2, 4, 2, 3)])
 def test_switch_glu(T, k, E, bits_gu, bits_d):
     H, I, gs = 256, 128, 64
     g = _stack(E, I, H, bits_gu, gs, seed=1)
