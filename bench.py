@@ -39,6 +39,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true")
     p.add_argument("--only", default="", help="comma list of extra workloads to run")
+    p.add_argument("--profile", choices=("gateup", "copy"), default=None,
+                   help="run only the dominant kernel (gateup) or a plain 256 MiB copy (copy), "
+                        "eagerly, for rocprofv3 counter passes; prints one JSON line")
     return p.parse_args()
 
 
@@ -82,21 +85,30 @@ def randn(shape, std, gen, dtype=None):
 
 
 def timed(fn, steps, warmup):
-    """Mean ms per call of fn(i) over `steps` calls, HIP events on torch's current stream
-    (the stream every jangq_amd launch uses)."""
+    """Mean ms per step of fn(0), ..., fn(steps - 1).
+
+    The W warmup calls run eagerly; the K timed calls are captured into one HIP graph and
+    replayed once, bracketed by HIP events on torch's current stream (the stream every
+    jangq_amd launch and the replay use), so host launch overhead is not measured."""
     import torch
 
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn(i)
+    torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record()
-    for i in range(steps):
-        fn(i)
+    g.replay()
     t1.record()
     torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps
+    ms = t0.elapsed_time(t1) / steps
+    del g
+    return ms
 
 
 def copies_for(nbytes):
@@ -286,6 +298,52 @@ def cpu_baseline_c2(max_seconds=30.0):
             "dequant_s": round(t_deq, 3), "matmul_s": round(t_mm, 3)}
 
 
+# ----------------------------------------------------------------------------- counters
+
+TRAFFIC_FILE = ROOT / "profiles" / "gateup_c2_m1_traffic.txt"
+
+
+def traffic_from_profile():
+    """HBM bytes per gate|up launch from the committed counter summary (FETCH_SIZE and
+    WRITE_SIZE passes, each scaled by the copy-kernel calibration), or None."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def profile_run(kind, steps):
+    """Eager launches of one kernel for a counter pass (no graph: counters are per dispatch)."""
+    import torch
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(200)
+    if kind == "copy":
+        n = 256 << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").random_(generator=gen)
+        dst = torch.empty_like(src)
+        for _ in range(steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return {"profile": "copy", "bytes_read": n, "bytes_written": n, "launches": steps}
+    import jangq_amd as jq
+
+    layer, acts, _, _ = c2_block(gen, 1)
+    R = copies_for(layer["g"].nbytes() + layer["u"].nbytes())
+    gs = [(layer["g"], layer["u"])] + [(layer["g"].clone(), layer["u"].clone())
+                                      for _ in range(R - 1)]
+    for i in range(steps):
+        g, u = gs[i % R]
+        jq.quantized_matmul_multi(acts[0], [g.tup(), u.tup()])
+    torch.cuda.synchronize()
+    x = acts[0]
+    nb = layer["g"].nbytes() + layer["u"].nbytes() + 2 * x.numel() + 2 * 2 * 14336
+    return {"profile": "gateup", "algorithmic_bytes": nb, "launches": steps, "copies": R}
+
+
 # ----------------------------------------------------------------------------- main
 
 
@@ -305,6 +363,9 @@ def main():
 
         jb.build()
     torch.cuda.set_device(0)
+    if args.profile:
+        print(json.dumps(profile_run(args.profile, args.steps)))
+        return
     gen = torch.Generator(device="cuda")
     gen.manual_seed(200)
 
@@ -375,7 +436,7 @@ def main():
             "frac": round(res["gu_gbs"] / HBM_PEAK_GBS, 4),
             "avg_launch_ms": round(res["gu_ms"], 5),
             "algorithmic_bytes": res["gu_bytes"],
-            "traffic": None,
+            "traffic": traffic_from_profile(),
         },
         "cpu_baseline": cpu,
         "extra": extra,

@@ -30,7 +30,11 @@ COMMON_FLAGS = [
     f"-I{ROOT / 'include'}",
 ]
 # Per-file extra flags: the codec must round q*s and +b separately (no FMA contraction).
-EXTRA = {"jq_codec.hip": ["-ffp-contract=off"]}
+EXTRA = {
+    "jq_codec.hip": ["-ffp-contract=off"],
+    # decode kernels: keep MFMA results in VGPRs (no accumulator-register round trips)
+    "jq_dec.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def hipcc() -> str:

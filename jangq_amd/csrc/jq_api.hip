@@ -1,5 +1,6 @@
-// Dense matmul entry points: dispatch between the decode GEMV (M <= 4, or any shape the
-// matrix-core kernel does not take) and the matrix-core GEMM.
+// Dense matmul entry points: dispatch between the vector-ALU decode GEMV (M <= 4), the
+// decode-shaped matrix-core kernel (a few more rows), the matrix-core GEMM and, for shapes
+// none of those takes, the generic GEMV.
 #include "jq_common.h"
 #include "jq_qmv.h"
 
@@ -9,6 +10,15 @@ int dense_one(const void* x, int xd, const uint32_t* codes, const void* scales,
               const void* biases, int sb, int bits, int gs, int64_t M, int64_t N, int64_t K,
               void* y, int yd, hipStream_t st) {
   const bool mfma_ok = (xd == JQ_BF16 || xd == JQ_F16) && K % 128 == 0;
+  const int Mi = (int)(M < (1 << 30) ? M : (1 << 30));
+  if (jqk::gemv_ok(Mi, K, bits, gs, xd, sb)) {
+    jqk::QmvBatch b;
+    b.M = Mi;
+    b.K = (int)K;
+    b.p[0].x = x; b.p[0].codes = codes; b.p[0].scales = scales; b.p[0].biases = biases;
+    b.p[0].y = y; b.p[0].N = N;
+    return jqk::gemv_launch(b, 1, bits, gs, xd, sb, yd, st);
+  }
   if (jqk::dec_dense_ok((int)(M < (1 << 30) ? M : (1 << 30)), K, gs, xd, sb)) {
     jqk::QmvBatch b;
     b.M = (int)M;
@@ -103,9 +113,10 @@ int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
   bool same = count <= jqk::kMaxProblems;
   for (int i = 1; i < count && same; ++i)
     same = bits[i] == bits[0] && group_size[i] == group_size[0] && M[i] == M[0] && K[i] == K[0];
-  const bool dec = same && jqk::dec_dense_ok((int)(M[0] < (1 << 30) ? M[0] : (1 << 30)), K[0],
-                                             group_size[0], x_dtype, sb_dtype);
-  if (dec || (same && M[0] >= 1 && M[0] <= 4 && K[0] > 0)) {
+  const int M0 = (int)(M[0] < (1 << 30) ? M[0] : (1 << 30));
+  const bool gemv = same && jqk::gemv_ok(M0, K[0], bits[0], group_size[0], x_dtype, sb_dtype);
+  const bool dec = same && jqk::dec_dense_ok(M0, K[0], group_size[0], x_dtype, sb_dtype);
+  if (gemv || dec || (same && M[0] >= 1 && M[0] <= 4 && K[0] > 0)) {
     jqk::QmvBatch b;
     b.M = (int)M[0];
     b.K = (int)K[0];
@@ -120,6 +131,7 @@ int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
       b.p[n].N = N[i];
       ++n;
     }
+    if (gemv) return jqk::gemv_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
     if (dec) return jqk::dec_dense_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
     return jqk::qmv_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
   }

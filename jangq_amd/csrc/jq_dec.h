@@ -1,20 +1,28 @@
 // Decode-shaped matrix-core kernels (few activation rows): shared device code.
 //
-// Work unit: a 16-row tile of W over a K range, for up to TPB activation rows. Every lane
+// Work unit: RT tiles of 16 W rows over a K range, for up to TPB activation rows. Every lane
 // streams its own row's codes straight from HBM into MFMA B fragments: lane (r = l%16,
 // g = l/16) loads 32-code unit g of each 128-code step of row r (BITS whole words), so one
 // wave load instruction reads 16 rows x 4*BITS*4 contiguous bytes and nothing is staged in
-// LDS. The unit's four 8-code chunks become four B fragments (exact 16-bit "magic" values
-// 2^B + q, see jq_common.h).
+// LDS.
 //
-// A 128-code step spans GSTEP = 128/gs groups, and lane group g holds codes of group
-// g / (4/GSTEP). Instead of splitting each MFMA by group, the group index is folded into the
-// MFMA's M dimension: A row m' = GSTEP*t + j carries token t's activations only in the lane
-// groups of group j (zeros elsewhere). One 16x16x32 MFMA per chunk then yields, for every
-// (token, group) row, that group's magic dot product D; the constant B = 1 gives the
-// activation sums X the same way. A lane's four output rows m' = 4*(l/16) + i belong to
-// group i % GSTEP, so the per-group affine terms  s*D + (b - 2^B s)*X  use scales that are
-// compile-time indexed per accumulator slot. Tokens per MFMA block: TPB = 16 / GSTEP.
+// Codes become exact 16-bit floats without int->float conversion: a code c placed at mantissa
+// offset p under the exponent E makes the value 2^E' + c with the code's own offset term. For
+// bf16 activations and 2/3/4-bit codes each code gets its own offset p (a "schedule"), so one
+// funnel-shifted 32-bit window of the unit feeds up to three dwords with a single
+// and-or each (20 / 25 / 28 instructions per 32 codes, found by exhaustive search); the
+// per-slot offsets 2^(7-p) form a constant B operand. Other widths (and f16 activations) use
+// one offset 2^B for every code (jq_common.h "magic pairs").
+//
+// A 128-code step spans GSTEP = 128/gs groups; lane group g holds codes of group
+// g / (4/GSTEP). The group index is folded into the MFMA's M dimension: A row m' = GSTEP*t + j
+// carries token t's activations only in the lane groups of group j (zeros elsewhere). Per
+// step, with A_f the four A fragments:
+//   O = sum_f A_f . BO_f   (-offsets)      X = sum_f A_f . 1   (activation sums)
+//   D = O + sum_f A_f . B_f                 (= sum q*x exactly, per (token, group) row)
+//   acc += s_g * D + b_g * X
+// A lane's four output rows m' = 4*(l/16) + i belong to group i % GSTEP, so the scales are
+// indexed at compile time per accumulator slot. Tokens per MFMA block: TPB = 16 / GSTEP.
 #pragma once
 
 #include "jq_common.h"
@@ -23,37 +31,162 @@ namespace jqd {
 
 using namespace jq;
 
+// ----------------------------------------------------------------------------- schedules
+
+// Pair i (0..15) of a unit: dword i = (code a[i] as lo half, code b[i] as hi half), built
+// from the window starting at bit s[i] with the codes at mantissa offsets pa[i] / pb[i].
+// MFMA field f uses dwords 4f..4f+3.
+struct Sched {
+  int a[16], b[16], s[16], pa[16], pb[16];
+};
+
+// 2-bit: 4 shifted windows + 16 and-or.
+constexpr Sched kSched2 = {
+    {0, 1, 2, 3, 4, 5, 6, 7, 16, 17, 18, 19, 20, 21, 22, 23},
+    {8, 9, 10, 11, 12, 13, 14, 15, 24, 25, 26, 27, 28, 29, 30, 31},
+    {0, 0, 0, 3, 3, 9, 9, 9, 32, 32, 32, 35, 35, 41, 41, 41},
+    {0, 2, 4, 3, 5, 1, 3, 5, 0, 2, 4, 3, 5, 1, 3, 5},
+    {0, 2, 4, 3, 5, 1, 3, 5, 0, 2, 4, 3, 5, 1, 3, 5}};
+// 3-bit: 9 shifted windows + 16 and-or.
+constexpr Sched kSched3 = {
+    {0, 1, 2, 3, 4, 5, 12, 13, 14, 15, 16, 22, 23, 24, 25, 26},
+    {6, 7, 8, 9, 10, 11, 17, 18, 19, 20, 21, 27, 28, 29, 30, 31},
+    {0, 1, 4, 7, 10, 13, 32, 38, 38, 44, 44, 64, 68, 68, 74, 74},
+    {0, 2, 2, 2, 2, 2, 4, 1, 4, 1, 4, 2, 1, 4, 1, 4},
+    {2, 4, 4, 4, 4, 4, 3, 0, 3, 0, 3, 1, 0, 3, 0, 3}};
+// 4-bit: pairs (c, c+4) at offset 0, 12 shifted windows + 16 and-or.
+constexpr Sched kSched4 = {
+    {0, 1, 2, 3, 8, 9, 10, 11, 16, 17, 18, 19, 24, 25, 26, 27},
+    {4, 5, 6, 7, 12, 13, 14, 15, 20, 21, 22, 23, 28, 29, 30, 31},
+    {0, 4, 8, 12, 32, 36, 40, 44, 64, 68, 72, 76, 96, 100, 104, 108},
+    {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0},
+    {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}};
+
+template <int BITS>
+constexpr const Sched& sched() {
+  if constexpr (BITS == 2) return kSched2;
+  else if constexpr (BITS == 3) return kSched3;
+  else return kSched4;
+}
+
 template <int BITS_, int GS_, int XDT_>
 struct Dc {
   static constexpr int BITS = BITS_, GS = GS_, XDT = XDT_;
   static constexpr int GSTEP = 128 / GS;   // groups per 128-code step
   static constexpr int TPB = 16 / GSTEP;   // activation rows per MFMA block
   static constexpr int LPG = 4 / GSTEP;    // lane groups per group
-  static constexpr bool NIB = BITS == 8 && XDT == JQ_BF16;  // 8-bit codes as two nibbles
-  static constexpr bool TWO = BITS == 2;   // 2-bit: pairs 8 codes apart in one word
-  static constexpr float OFF = NIB ? 272.f : (float)(1 << BITS);
+  static constexpr bool SCHED = XDT == JQ_BF16 && BITS >= 2 && BITS <= 4;  // per-code offsets
+  static constexpr bool NIB = BITS == 8 && XDT == JQ_BF16;                // two nibbles
+  static constexpr bool TWO = !SCHED && BITS == 2;  // f16 2-bit: pairs 8 codes apart
   static constexpr uint32_t ONE2 = XDT == JQ_BF16 ? 0x3F803F80u : 0x3C003C00u;
 };
 
-// B fragment(s) of field C (0..3) of a unit. Field layout:
-//   BITS != 2: chunk C = codes 8C..8C+7, pairs (c_p, c_{p+4})
-//   BITS == 2: word C/2, pairs (c_j, c_{j+8}) for j = 4*(C%2) + p
-template <class D, int C>
-JQ_DEV void b_frag(const uint32_t* w, u32x4& b, u32x4& bh) {
-  if constexpr (D::NIB) {
+// Code indices (within the lane's 32-code unit) of dword p of field f: lo / hi halves.
+template <class D>
+constexpr int code_lo(int f, int p) {
+  if constexpr (D::SCHED) return sched<D::BITS>().a[4 * f + p];
+  else if constexpr (D::TWO) return 16 * (f >> 1) + 4 * (f & 1) + p;
+  else return 8 * f + p;
+}
+template <class D>
+constexpr int code_hi(int f, int p) {
+  if constexpr (D::SCHED) return sched<D::BITS>().b[4 * f + p];
+  else if constexpr (D::TWO) return 16 * (f >> 1) + 4 * (f & 1) + p + 8;
+  else return 8 * f + p + 4;
+}
+
+// 16-bit value -2^e of format FMT.
+template <int FMT>
+constexpr uint32_t neg_pow2(int e) {
+  return FMT == JQ_BF16 ? (0x8000u | ((uint32_t)(127 + e) << 7))
+                        : (0x8000u | ((uint32_t)(15 + e) << 10));
+}
+
+// Constant B fragment of field f holding minus each slot's offset.
+template <class D>
+constexpr uint32_t bo_dword(int f, int p) {
+  if constexpr (D::SCHED) {
+    const Sched& S = sched<D::BITS>();
+    return neg_pow2<JQ_BF16>(7 - S.pa[4 * f + p]) | (neg_pow2<JQ_BF16>(7 - S.pb[4 * f + p]) << 16);
+  } else if constexpr (D::NIB) {
+    return 0xC388C388u;  // bf16 -272 (= -(256 + 16)), exact
+  } else {
+    return neg_pow2<D::XDT>(D::BITS) | (neg_pow2<D::XDT>(D::BITS) << 16);
+  }
+}
+
+// Magic bases of a scheduled unit, pinned in VGPRs (gfx9 VOP3 instructions take at most one
+// scalar operand, so the and-or's mask is the scalar and the base must be a vector register).
+template <class D>
+struct Bases {
+  uint32_t v[16];
+};
+
+// First pair index with the same (pa, pb) as pair i: equal bases share one register.
+template <int BITS>
+constexpr int base_rep(int i) {
+  const Sched& S = sched<BITS>();
+  for (int j = 0; j < i; ++j)
+    if (S.pa[j] == S.pa[i] && S.pb[j] == S.pb[i]) return j;
+  return i;
+}
+
+template <class D>
+JQ_DEV Bases<D> make_bases() {
+  Bases<D> r;
+  if constexpr (D::SCHED) {
+    const Sched& S = sched<D::BITS>();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (base_rep<D::BITS>(i) == i) {
+        r.v[i] = ((uint32_t)(134 - S.pa[i]) << 7) | ((uint32_t)(134 - S.pb[i]) << 23);
+        asm volatile("" : "+v"(r.v[i]));
+      } else {
+        r.v[i] = r.v[base_rep<D::BITS>(i)];
+      }
+    }
+  }
+  return r;
+}
+
+// Bits [s, s+32) of the unit (zeros past its end).
+template <int BITS, int S>
+JQ_DEV uint32_t window(const uint32_t* w) {
+  constexpr int lo = S >> 5, sh = S & 31;
+  if constexpr (sh == 0) return w[lo];
+  else if constexpr (lo + 1 < BITS) return __builtin_amdgcn_alignbit(w[lo + 1], w[lo], sh);
+  else return w[lo] >> sh;
+}
+
+template <class D, int I>
+JQ_DEV uint32_t sched_dword(const uint32_t* w, const Bases<D>& bs) {
+  constexpr const Sched& S = sched<D::BITS>();
+  constexpr uint32_t m = (1u << D::BITS) - 1u;
+  constexpr uint32_t mask = (m << S.pa[I]) | (m << (16 + S.pb[I]));
+  return (window<D::BITS, S.s[I]>(w) & mask) | bs.v[I];
+}
+
+// B fragment(s) of field F of a unit.
+template <class D, int F>
+JQ_DEV void b_frag(const uint32_t* w, const Bases<D>& bs, u32x4& b, u32x4& bh) {
+  if constexpr (D::SCHED) {
+    b = u32x4{sched_dword<D, 4 * F>(w, bs), sched_dword<D, 4 * F + 1>(w, bs),
+              sched_dword<D, 4 * F + 2>(w, bs), sched_dword<D, 4 * F + 3>(w, bs)};
+    bh = b;
+  } else if constexpr (D::NIB) {
     uint32_t lo[4], hi[4];
-    chunk8_nibble_pairs(w[2 * C], w[2 * C + 1], lo, hi);
+    chunk8_nibble_pairs(w[2 * F], w[2 * F + 1], lo, hi);
     b = u32x4{lo[0], lo[1], lo[2], lo[3]};
     bh = u32x4{hi[0], hi[1], hi[2], hi[3]};
   } else if constexpr (D::TWO) {
     using Mg = Magic<D::XDT, 2>;
     constexpr int sh = Mg::shift;
     constexpr uint32_t pm = (3u << sh) | (3u << (sh + 16));
-    const uint32_t word = w[C >> 1];
+    const uint32_t word = w[F >> 1];
     uint32_t o[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      const int j = 4 * (C & 1) + p;
+      const int j = 4 * (F & 1) + p;
       const int s = 2 * j - sh;
       const uint32_t t = s >= 0 ? (word >> s) : (word << (-s));
       o[p] = (t & pm) | Mg::base;
@@ -62,106 +195,146 @@ JQ_DEV void b_frag(const uint32_t* w, u32x4& b, u32x4& bh) {
     bh = b;
   } else {
     uint32_t o[4];
-    unit_chunk_pairs<D::XDT, D::BITS, C>(w, o);
+    unit_chunk_pairs<D::XDT, D::BITS, F>(w, o);
     b = u32x4{o[0], o[1], o[2], o[3]};
     bh = b;
   }
 }
 
-// A fragment of field C for lane group lg from the activation row `xr` (16-bit elements,
-// already offset to the step). Zero when the lane is inactive.
-template <class D, int C>
-JQ_DEV u32x4 a_frag(const uint16_t* xr, bool act, int lg) {
-  if (!act) return u32x4{0u, 0u, 0u, 0u};
-  if constexpr (D::TWO) {
-    const int a = 32 * lg + 16 * (C >> 1) + 4 * (C & 1);
-    const uint2 lo = *(const uint2*)(xr + a);
-    const uint2 hi = *(const uint2*)(xr + a + 8);
-    return u32x4{__builtin_amdgcn_perm(hi.x, lo.x, 0x05040100u),
-                 __builtin_amdgcn_perm(hi.x, lo.x, 0x07060302u),
-                 __builtin_amdgcn_perm(hi.y, lo.y, 0x05040100u),
-                 __builtin_amdgcn_perm(hi.y, lo.y, 0x07060302u)};
-  } else {
-    const uint4 v = *(const uint4*)(xr + 32 * lg + 8 * C);
-    const uint32_t raw[4] = {v.x, v.y, v.z, v.w};
-    uint32_t pr[4];
-    pair_activations(raw, pr);
-    return u32x4{pr[0], pr[1], pr[2], pr[3]};
+// ----------------------------------------------------------------------------- activations
+
+// Raw activations of one step for this lane's A row: the 32 values of lane group lg,
+// x[32*lg .. 32*lg+31] of the step, as 16 dwords (x_{2i}, x_{2i+1}).
+struct XRaw {
+  uint32_t d[16];
+};
+
+// 64 zero bytes: lanes that feed no activation read these instead of branching (a branch
+// around a load makes the compiler wait for every outstanding load at the join).
+static __device__ const uint4 kZeroRow[4] = {};
+
+typedef const __attribute__((address_space(1))) u32x4 global_u32x4;
+
+JQ_DEV void load_xraw(const uint16_t* p, XRaw& r) {
+  // Global (not flat) loads: a flat load also counts against the LDS/scalar counter and
+  // would force a full wait on every step.
+  global_u32x4* q = (global_u32x4*)p;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 v = q[i];
+    r.d[4 * i] = v.x; r.d[4 * i + 1] = v.y; r.d[4 * i + 2] = v.z; r.d[4 * i + 3] = v.w;
   }
 }
 
-// Scales / biases of GSTEP consecutive groups starting at element `g0` of a 16-bit sidecar row.
-template <class D, int SB>
-JQ_DEV void load_sb(const uint16_t* srow, const uint16_t* brow, int g0, float s[D::GSTEP],
-                    float b[D::GSTEP]) {
-  uint32_t sw[(D::GSTEP + 1) / 2], bw[(D::GSTEP + 1) / 2];
+// A dword (x_a, x_b) from the raw dwords: one byte permute.
+template <int A, int B>
+JQ_DEV uint32_t xpair(const XRaw& r) {
+  constexpr uint32_t lo = (A & 1) ? 0x0302u : 0x0100u;
+  constexpr uint32_t hi = (B & 1) ? 0x0706u : 0x0504u;
+  return __builtin_amdgcn_perm(r.d[B >> 1], r.d[A >> 1], lo | (hi << 16));
+}
+
+template <class D, int F>
+JQ_DEV u32x4 a_frag(const XRaw& r) {
+  return u32x4{xpair<code_lo<D>(F, 0), code_hi<D>(F, 0)>(r),
+               xpair<code_lo<D>(F, 1), code_hi<D>(F, 1)>(r),
+               xpair<code_lo<D>(F, 2), code_hi<D>(F, 2)>(r),
+               xpair<code_lo<D>(F, 3), code_hi<D>(F, 3)>(r)};
+}
+
+// ----------------------------------------------------------------------------- scales
+
+// Raw 16-bit scale / bias words of the GSTEP groups of one step.
+template <class D>
+struct SBRaw {
+  uint32_t s[(D::GSTEP + 1) / 2], b[(D::GSTEP + 1) / 2];
+};
+
+template <class D>
+JQ_DEV void load_sbraw(const uint16_t* srow, const uint16_t* brow, int g0, SBRaw<D>& r) {
   if constexpr (D::GSTEP == 1) {
-    sw[0] = srow[g0];
-    bw[0] = brow[g0];
+    r.s[0] = srow[g0];
+    r.b[0] = brow[g0];
   } else if constexpr (D::GSTEP == 2) {
-    sw[0] = *(const uint32_t*)(srow + g0);
-    bw[0] = *(const uint32_t*)(brow + g0);
+    r.s[0] = *(const uint32_t*)(srow + g0);
+    r.b[0] = *(const uint32_t*)(brow + g0);
   } else {
     const uint2 a = *(const uint2*)(srow + g0), c = *(const uint2*)(brow + g0);
-    sw[0] = a.x; sw[1] = a.y; bw[0] = c.x; bw[1] = c.y;
-  }
-#pragma unroll
-  for (int j = 0; j < D::GSTEP; ++j) {
-    const uint32_t hs = (sw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
-    const uint32_t hb = (bw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
-    if constexpr (SB == JQ_BF16) {
-      s[j] = bf16_bits_to_f32(hs);
-      b[j] = bf16_bits_to_f32(hb);
-    } else {
-      s[j] = f16_bits_to_f32((uint16_t)hs);
-      b[j] = f16_bits_to_f32((uint16_t)hb);
-    }
+    r.s[0] = a.x; r.s[1] = a.y; r.b[0] = c.x; r.b[1] = c.y;
   }
 }
 
-// Partial sums of one 16-row tile over steps [s0, s1) for NB weight matrices sharing the
-// activations. crow/srow/brow: this lane's W row (column of the output) per matrix.
-// xr: this lane's activation row (token of A row l%16), act: whether the lane feeds A.
-template <class D, int SB, int NB>
-JQ_DEV void dec_tile(const uint16_t* xr, bool act, const uint32_t* const* crow,
-                     const uint16_t* const* srow, const uint16_t* const* brow, int s0, int s1,
-                     int lg, f32x4* acc) {
-  constexpr int BITS = D::BITS;
+template <int SB>
+JQ_DEV float half_to_f32(uint32_t w, int hi) {
+  if constexpr (SB == JQ_BF16) {
+    return __uint_as_float(hi ? (w & 0xFFFF0000u) : (w << 16));
+  } else {
+    return f16_bits_to_f32((uint16_t)(hi ? (w >> 16) : w));
+  }
+}
+
+// ----------------------------------------------------------------------------- main loop
+
+// What one step reads from HBM for RT row tiles x NB matrices: codes and their scales.
+template <class D, int NB, int RT>
+struct CodeStage {
+  UnitWords<D::BITS> c[NB][RT];
+  SBRaw<D> sb[NB][RT];
+};
+
+struct TileRows {
+  const uint32_t* c;  // this lane's W row, codes
+  const uint16_t* s;  // scales row
+  const uint16_t* b;  // biases row
+};
+
+template <class D, int NB, int RT>
+JQ_DEV void load_codes(const TileRows (&rows)[NB][RT], int s, int lg, CodeStage<D, NB, RT>& st) {
+#pragma unroll
+  for (int q = 0; q < NB; ++q)
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      st.c[q][r] = load_unit<D::BITS>(rows[q][r].c + (s * 4 + lg) * D::BITS);
+      load_sbraw<D>(rows[q][r].s, rows[q][r].b, s * D::GSTEP, st.sb[q][r]);
+    }
+}
+
+template <class D, int SB, int NB, int RT>
+JQ_DEV void compute_stage(const CodeStage<D, NB, RT>& st, const XRaw& xr, const Bases<D>& bs,
+                          f32x4 (&acc)[NB][RT]) {
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   const u32x4 ones = {D::ONE2, D::ONE2, D::ONE2, D::ONE2};
-  UnitWords<BITS> cur[NB], nxt[NB];
-  if (s0 < s1) {
+  const u32x4 A0 = a_frag<D, 0>(xr), A1 = a_frag<D, 1>(xr);
+  const u32x4 A2 = a_frag<D, 2>(xr), A3 = a_frag<D, 3>(xr);
+  f32x4 X = mfma16<D::XDT>(A0, ones, zero);
+  X = mfma16<D::XDT>(A1, ones, X);
+  X = mfma16<D::XDT>(A2, ones, X);
+  X = mfma16<D::XDT>(A3, ones, X);
+  constexpr u32x4 BO0 = {bo_dword<D>(0, 0), bo_dword<D>(0, 1), bo_dword<D>(0, 2), bo_dword<D>(0, 3)};
+  constexpr u32x4 BO1 = {bo_dword<D>(1, 0), bo_dword<D>(1, 1), bo_dword<D>(1, 2), bo_dword<D>(1, 3)};
+  constexpr u32x4 BO2 = {bo_dword<D>(2, 0), bo_dword<D>(2, 1), bo_dword<D>(2, 2), bo_dword<D>(2, 3)};
+  constexpr u32x4 BO3 = {bo_dword<D>(3, 0), bo_dword<D>(3, 1), bo_dword<D>(3, 2), bo_dword<D>(3, 3)};
+  f32x4 O = mfma16<D::XDT>(A0, BO0, zero);
+  O = mfma16<D::XDT>(A1, BO1, O);
+  O = mfma16<D::XDT>(A2, BO2, O);
+  O = mfma16<D::XDT>(A3, BO3, O);
 #pragma unroll
-    for (int q = 0; q < NB; ++q) cur[q] = load_unit<BITS>(crow[q] + (s0 * 4 + lg) * BITS);
-  }
-  for (int s = s0; s < s1; ++s) {
-    if (s + 1 < s1) {
+  for (int q = 0; q < NB; ++q)
 #pragma unroll
-      for (int q = 0; q < NB; ++q) nxt[q] = load_unit<BITS>(crow[q] + ((s + 1) * 4 + lg) * BITS);
-    }
-    const uint16_t* xs = xr + s * 128;
-    const u32x4 A0 = a_frag<D, 0>(xs, act, lg), A1 = a_frag<D, 1>(xs, act, lg);
-    const u32x4 A2 = a_frag<D, 2>(xs, act, lg), A3 = a_frag<D, 3>(xs, act, lg);
-    f32x4 X = mfma16<D::XDT>(A0, ones, zero);
-    X = mfma16<D::XDT>(A1, ones, X);
-    X = mfma16<D::XDT>(A2, ones, X);
-    X = mfma16<D::XDT>(A3, ones, X);
-#pragma unroll
-    for (int q = 0; q < NB; ++q) {
-      float sc[D::GSTEP], bi[D::GSTEP];
-      load_sb<D, SB>(srow[q], brow[q], s * D::GSTEP, sc, bi);
+    for (int r = 0; r < RT; ++r) {
+      const uint32_t* w = st.c[q][r].w;
       u32x4 B, BH;
-      b_frag<D, 0>(cur[q].w, B, BH);
-      f32x4 Dd = mfma16<D::XDT>(A0, B, zero);
-      f32x4 Dh = zero;
+      f32x4 Dd, Dh = zero;
+      b_frag<D, 0>(w, bs, B, BH);
+      Dd = mfma16<D::XDT>(A0, B, O);
       if constexpr (D::NIB) Dh = mfma16<D::XDT>(A0, BH, zero);
-      b_frag<D, 1>(cur[q].w, B, BH);
+      b_frag<D, 1>(w, bs, B, BH);
       Dd = mfma16<D::XDT>(A1, B, Dd);
       if constexpr (D::NIB) Dh = mfma16<D::XDT>(A1, BH, Dh);
-      b_frag<D, 2>(cur[q].w, B, BH);
+      b_frag<D, 2>(w, bs, B, BH);
       Dd = mfma16<D::XDT>(A2, B, Dd);
       if constexpr (D::NIB) Dh = mfma16<D::XDT>(A2, BH, Dh);
-      b_frag<D, 3>(cur[q].w, B, BH);
+      b_frag<D, 3>(w, bs, B, BH);
       Dd = mfma16<D::XDT>(A3, B, Dd);
       if constexpr (D::NIB) {
         Dh = mfma16<D::XDT>(A3, BH, Dh);
@@ -171,34 +344,78 @@ JQ_DEV void dec_tile(const uint16_t* xr, bool act, const uint32_t* const* crow,
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = i % D::GSTEP;
-        const float c = fmaf(-D::OFF, sc[j], bi[j]);
-        acc[q][i] = fmaf(sc[j], Dd[i], fmaf(c, X[i], acc[q][i]));
+        const float sc = half_to_f32<SB>(st.sb[q][r].s[j >> 1], j & 1);
+        const float bi = half_to_f32<SB>(st.sb[q][r].b[j >> 1], j & 1);
+        acc[q][r][i] = fmaf(sc, Dd[i], fmaf(bi, X[i], acc[q][r][i]));
       }
     }
+}
+
+// Steps of codes kept in flight per wave: about 4 KB per row tile (even, >= 2). The grids
+// of decode-shaped problems are too small to hide HBM latency with occupancy alone.
+template <int BITS>
+constexpr int code_depth() {
+  return BITS <= 2 ? 8 : BITS <= 3 ? 6 : BITS <= 6 ? 4 : 2;
+}
+
+// Partial sums of RT 16-row tiles over steps [s0, s1) for NB weight matrices sharing the
+// activations. rows: this lane's W rows. xr: this lane's activation row (token of A row
+// l%16), act: whether the lane feeds A. Codes and scales are fetched DEPTH steps ahead in a
+// register ring (static indices after unrolling), activations (L2-resident) one step ahead.
+// Every load is unconditional (indices clamped to the last step, inactive lanes read
+// zeros), so the loads of later steps stay in flight while a step is computed.
+template <class D, int SB, int NB, int RT>
+JQ_DEV void dec_tile(const uint16_t* xr, bool act, const TileRows (&rows)[NB][RT], int s0, int s1,
+                     int lg, f32x4 (&acc)[NB][RT]) {
+  constexpr int DEPTH = code_depth<D::BITS>();
+  if (s0 >= s1) return;
+  const int last = s1 - 1;
+  const Bases<D> bs = make_bases<D>();
+  const uint16_t* xl = xr + 32 * lg;
+  const uint16_t* zero = (const uint16_t*)kZeroRow;
+  CodeStage<D, NB, RT> ring[DEPTH];
 #pragma unroll
-    for (int q = 0; q < NB; ++q) cur[q] = nxt[q];
+  for (int d = 0; d < DEPTH; ++d) load_codes<D, NB, RT>(rows, min(s0 + d, last), lg, ring[d]);
+  XRaw xa, xb;
+  load_xraw(act ? xl + s0 * 128 : zero, xa);
+  for (int s = s0;; s += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int t = s + d;
+      const uint16_t* xn = act ? xl + min(t + 1, last) * 128 : zero;
+      if (d & 1) {
+        load_xraw(xn, xa);
+        compute_stage<D, SB, NB, RT>(ring[d], xb, bs, acc);
+      } else {
+        load_xraw(xn, xb);
+        compute_stage<D, SB, NB, RT>(ring[d], xa, bs, acc);
+      }
+      load_codes<D, NB, RT>(rows, min(t + DEPTH, last), lg, ring[d]);
+      if (t + 1 >= s1) return;
+    }
   }
 }
 
-// Sum the partials of the 4 waves of a block (each wave covered a quarter of K). Returns
-// the total in wave 0's registers. red: LDS scratch of 4 * NB * 256 floats.
-template <int NB>
-JQ_DEV void block_reduce4(f32x4* acc, float* red) {
+// Sum the partials of the KW waves of a block (each covered a K range). Returns the total
+// in wave 0's registers. red: LDS scratch of (KW-1) * N4 * 256 floats (N4 = accumulators).
+template <int KW, int N4>
+JQ_DEV void block_reduce(f32x4* acc, float* red) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave > 0) {
 #pragma unroll
-  for (int q = 0; q < NB; ++q)
+    for (int q = 0; q < N4; ++q)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[((wave * NB + q) * 4 + i) * 64 + lane] = acc[q][i];
+      for (int i = 0; i < 4; ++i) red[(((wave - 1) * N4 + q) * 4 + i) * 64 + lane] = acc[q][i];
+  }
   __syncthreads();
   if (wave == 0) {
 #pragma unroll
-    for (int q = 0; q < NB; ++q)
+    for (int q = 0; q < N4; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float v = red[((0 * NB + q) * 4 + i) * 64 + lane];
-        v += red[((1 * NB + q) * 4 + i) * 64 + lane];
-        v += red[((2 * NB + q) * 4 + i) * 64 + lane];
-        v += red[((3 * NB + q) * 4 + i) * 64 + lane];
+        float v = acc[q][i];
+#pragma unroll
+        for (int w = 1; w < KW; ++w) v += red[(((w - 1) * N4 + q) * 4 + i) * 64 + lane];
         acc[q][i] = v;
       }
   }

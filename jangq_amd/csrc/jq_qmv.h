@@ -27,6 +27,11 @@ struct QmvBatch {
 int qmv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
                hipStream_t st);
 
+// Decode GEMV on the vector ALUs (jq_gemv.hip): M <= 4, bf16/f16 activations and scales.
+bool gemv_ok(int M, int64_t K, int bits, int gs, int xd, int sb);
+int gemv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
+                hipStream_t st);
+
 // Row-gathered operand description for the grouped (MoE) matrix-core launches.
 // Pairs are processed in expert-grouped order `order`; A row r of segment e is
 //   pair p = order[seg_off[e] + r / M], token row m = r % M
