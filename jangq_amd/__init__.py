@@ -15,9 +15,11 @@ from .ops import (  # noqa: F401
     switch_glu,
     unpack,
 )
+from ._lib import JangqError  # noqa: F401
 from .shapes import bit_inference, infer_bits_group_size  # noqa: F401
 
 __all__ = [
     "dequantize", "gather_qmm", "moe_route", "quantize", "quantized_matmul",
     "quantized_matmul_multi", "switch_glu", "unpack", "bit_inference", "infer_bits_group_size",
+    "JangqError",
 ]
