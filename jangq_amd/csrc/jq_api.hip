@@ -11,7 +11,7 @@ int dense_one(const void* x, int xd, const uint32_t* codes, const void* scales,
               void* y, int yd, hipStream_t st) {
   const bool mfma_ok = (xd == JQ_BF16 || xd == JQ_F16) && K % 128 == 0;
   const int Mi = (int)(M < (1 << 30) ? M : (1 << 30));
-  if (jqk::gemv_ok(Mi, K, bits, gs, xd, sb)) {
+  if (jqk::gemv_ok(Mi, K, N, bits, gs, xd, sb)) {
     jqk::QmvBatch b;
     b.M = Mi;
     b.K = (int)K;
@@ -114,7 +114,9 @@ int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
   for (int i = 1; i < count && same; ++i)
     same = bits[i] == bits[0] && group_size[i] == group_size[0] && M[i] == M[0] && K[i] == K[0];
   const int M0 = (int)(M[0] < (1 << 30) ? M[0] : (1 << 30));
-  const bool gemv = same && jqk::gemv_ok(M0, K[0], bits[0], group_size[0], x_dtype, sb_dtype);
+  int64_t maxN = 0;
+  for (int i = 0; i < count; ++i) maxN = N[i] > maxN ? N[i] : maxN;
+  const bool gemv = same && jqk::gemv_ok(M0, K[0], maxN, bits[0], group_size[0], x_dtype, sb_dtype);
   const bool dec = same && jqk::dec_dense_ok(M0, K[0], group_size[0], x_dtype, sb_dtype);
   if (gemv || dec || (same && M[0] >= 1 && M[0] <= 4 && K[0] > 0)) {
     jqk::QmvBatch b;

@@ -2,18 +2,19 @@
 // for a few activation rows (M <= 4; M <= 2 at 2 bits), bf16 or f16 activations, K up to 512
 // lane chunks. No matrix cores.
 //
-// Work split. A block of KW waves owns RB consecutive output rows. The row's packed codes are
-// cut into lane chunks of UPL whole 32-code units (UPL = 2 for 2-bit, so that every chunk is
-// 16 bytes; 1 otherwise: 12, 16, 20, 24 or 32 bytes). Wave w takes a contiguous range of
-// chunks and lane l the chunks l, l+64, ... of that range (J per lane), so each load
-// instruction of a wave reads one contiguous run of a row, and the lane's K slice is the same
-// for every row of the block.
+// Work split. A block of KW waves works on row blocks of RB consecutive output rows. A row's
+// packed codes are cut into lane chunks of UPL whole 32-code units (UPL = 2 for 2-bit, so that
+// every chunk is 16 bytes; 1 otherwise: 12, 16, 20, 24 or 32 bytes). Wave w takes a contiguous
+// range of chunks and lane l chunk l of that range, so each load instruction of a wave reads
+// one contiguous run of a row (buffer loads of 16 / 12 / 8 bytes per lane), and the lane's K
+// slice is the same for every row.
 //
-// Activation-stationary. The lane loads its K slice of x once per block and keeps it in
-// registers in the pairing the code unpack produces, together with two per-unit constants,
-// X = sum x and O = -sum offset_k x_k. The codes of all RB rows (plus their scales and biases)
-// are issued up front, in the order they are consumed, so one wave keeps RB rows of loads in
-// flight and waits on them one row at a time.
+// Activation-stationary and persistent. Blocks stay resident and walk row blocks b,
+// b + gridDim.x, ...; a lane loads its K slice of x once and keeps it in registers in the
+// pairing the code unpack produces, with two per-unit constants, X = sum x and
+// O = -sum offset_k x_k. The codes, scales and biases of the RB rows live in a rolling
+// register ring: row r of the next row block is issued as soon as row r of the current one
+// has been consumed, so RB rows of loads stay in flight through the reduction and the store.
 //
 // Arithmetic. Codes become exact 16-bit floats (offset_k + q_k) with mask-and-or only (the
 // per-code offset schedules for bf16 2/3/4-bit, the uniform 2^bits offset otherwise; 8-bit bf16
@@ -116,229 +117,303 @@ JQ_DEV float sb_to_f32(uint32_t h) {
   else return f16_bits_to_f32((uint16_t)h);
 }
 
-// Codes, scales and biases of one row for one lane: J chunks of UPL units (a scale and a
-// bias per unit; units of one group load the same element).
-template <int BITS, int UPL, int J>
-struct RowLoad {
-  uint32_t w[J][BITS * UPL];
-  uint32_t s[J][UPL], b[J][UPL];
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Raw buffer view of `bytes` bytes at p: loads past the end read zero and touch no memory.
+JQ_DEV Rsrc make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// The BITS*UPL code words of a lane chunk at byte voff of a row block. All offsets go into
+// the vector offset: the buffer range check covers it, not the scalar offset.
+template <int NW>
+JQ_DEV void load_chunk(Rsrc r, uint32_t voff, uint32_t* w) {
+  constexpr int soff = 0;
+  if constexpr (NW == 4) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+  } else if constexpr (NW == 8) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
+    w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+    w[4] = u[0]; w[5] = u[1]; w[6] = u[2]; w[7] = u[3];
+  } else if constexpr (NW == 3) {
+    const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, 0);
+    w[0] = v[0]; w[1] = v[1]; w[2] = v[2];
+  } else if constexpr (NW == 6) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, voff + 8 * i, soff, 0);
+      w[2 * i] = v[0]; w[2 * i + 1] = v[1];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NW; ++i) w[i] = __builtin_amdgcn_raw_buffer_load_b32(r, voff + 4 * i, soff, 0);
+  }
+}
+
+// Launch arguments: problems of one grouped launch share x, M, K and the dtypes; their row
+// blocks are numbered 0 .. rb_begin[nprob) in problem order.
+struct GemvArgs {
+  QmvBatch b;
+  int rb_begin[jqk::kMaxProblems + 1];
+  int nprob;
+  int ushift;    // log2(gs / 32)
+  int kwshift;   // log2(waves per block)
+  int yd;
 };
 
-template <int N>
-JQ_DEV void load_words(const uint32_t* __restrict__ p, uint32_t* w) {
-  if constexpr (N == 4) {
-    const u32x4 v = *(const u32x4*)p;
-    w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
-  } else if constexpr (N == 8) {
-    const u32x4 a = *(const u32x4*)p, c = *(const u32x4*)(p + 4);
-    w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
-    w[4] = c[0]; w[5] = c[1]; w[6] = c[2]; w[7] = c[3];
-  } else if constexpr (N == 6) {
-    const uint2 a = *(const uint2*)p, b = *(const uint2*)(p + 2), c = *(const uint2*)(p + 4);
-    w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y; w[4] = c.x; w[5] = c.y;
-  } else {
-#pragma unroll
-    for (int i = 0; i < N; ++i) w[i] = p[i];
-  }
-}
-
-// Block = KW waves (blockDim.x = 64 * KW, KW <= kMaxWaves); ushift = log2(gs / 32).
+// Block = KW waves (blockDim.x = 64 * KW, KW <= kMaxWaves).
 constexpr int kMaxWaves = 8;
 
-template <class D, int SB, int MT, int RB, int J>
-__global__ void __launch_bounds__(64 * kMaxWaves) gemv_kernel(QmvBatch batch, int ushift, int yd) {
+// Waves per block for a K: the fewest (a power of two) for which each lane holds one chunk.
+inline int gemv_waves(int64_t K, int bits, int* shift) {
+  const int upl = bits == 2 ? 2 : 1;
+  const int64_t C = K / (32 * upl);
+  int kw = 1, ks = 0;
+  while (64 * kw < C) kw *= 2, ++ks;
+  if (shift) *shift = ks;
+  return kw;
+}
+
+// One row of a lane's ring slot: the chunk's code words, and the scale and bias of each of
+// its units (units of one group load the same element).
+template <int NW, int UPL>
+struct RowSlot {
+  uint32_t w[NW];
+  uint32_t s[UPL], b[UPL];
+};
+
+// Persistent: block b handles row blocks b, b + gridDim.x, ... Each lane keeps a rolling
+// ring of the RB rows of its current row block in registers; row r of the next row block is
+// issued right after row r of the current one has been consumed, so RB rows of loads stay in
+// flight while the block computes, reduces and stores.
+template <class D, int SB, int MT, int RB>
+__global__ void __launch_bounds__(64 * kMaxWaves) gemv_kernel(GemvArgs a) {
   constexpr int BITS = D::BITS;
   constexpr int UPL = units_per_chunk<BITS>();
-  __shared__ float red[kMaxWaves][RB * MT];
-  const int KW = blockDim.x >> 6;
+  constexpr int NW = BITS * UPL;
+  __shared__ float red[2][kMaxWaves][RB * MT];
 
-  const QmvProblem& pb = batch.p[blockIdx.y];
-  const int64_t N = pb.N;
-  const int64_t row0 = (int64_t)blockIdx.x * RB;
-  if (row0 >= N) return;  // whole block
-  const int K = batch.K, M = batch.M;
+  const int total = a.rb_begin[a.nprob];
+  int it = blockIdx.x;
+  if (it >= total) return;  // whole block
+  const int KW = blockDim.x >> 6;
+  const int K = a.b.K, M = a.b.M;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int C = K / (32 * UPL);                  // chunks per row
-  const int CW = (C + KW - 1) / KW;              // chunks per wave
-  const int64_t P = (int64_t)K * BITS / 32;      // words per row
-  const int G = K >> (ushift + 5);
+  const int C = K / (32 * UPL);                       // chunks per row
+  const int CW = (C + KW - 1) >> a.kwshift;           // chunks per wave
+  const uint32_t rowbytes = (uint32_t)(K / 32) * BITS * 4;
+  const uint32_t sbrow = (uint32_t)(K >> (a.ushift + 5)) * 2;
 
-  // Lane chunks: active flag and clamped chunk index.
-  int cidx[J];
-  bool act[J];
+  const int c = wave * CW + lane;
+  const bool act = lane < CW && c < C;
+  const int ci = act ? c : 0;
+  const uint32_t voff = (uint32_t)ci * (4 * NW);
+  uint32_t vsb[UPL];
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int loc = lane + 64 * j;
-    const int c = wave * CW + loc;
-    act[j] = loc < CW && c < C;
-    cidx[j] = act[j] ? c : 0;
-  }
+  for (int t = 0; t < UPL; ++t) vsb[t] = (uint32_t)((ci * UPL + t) >> a.ushift) * 2;
 
-  // Activations first (so waiting for them does not wait for the codes).
-  jqd::XRaw xr[J][UPL][MT];
+  // Activations first (waiting for them does not wait for the codes).
+  jqd::XRaw xr[UPL][MT];
 #pragma unroll
-  for (int j = 0; j < J; ++j)
+  for (int t = 0; t < UPL; ++t)
 #pragma unroll
-    for (int t = 0; t < UPL; ++t)
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const int mm = m < M ? m : M - 1;
-        jqd::load_xraw((const uint16_t*)pb.x + (int64_t)mm * K + (int64_t)(cidx[j] * UPL + t) * 32,
-                       xr[j][t][m]);
-      }
+    for (int m = 0; m < MT; ++m) {
+      const int mm = m < M ? m : M - 1;
+      jqd::load_xraw((const uint16_t*)a.b.p[0].x + (int64_t)mm * K + (int64_t)(ci * UPL + t) * 32,
+                     xr[t][m]);
+    }
 
-  // All RB rows of codes, scales and biases, in consumption order.
-  RowLoad<BITS, UPL, J> rl[RB];
-  const uint32_t* __restrict__ codes = pb.codes;
-  const uint16_t* __restrict__ sc = (const uint16_t*)pb.scales;
-  const uint16_t* __restrict__ bi = (const uint16_t*)pb.biases;
+  // Row block `i`: its problem, first row and buffer views of its RB rows (rows past the
+  // problem's end read zero).
+  auto locate = [&](int i, int& p, int64_t& row0) {
+    p = 0;
+#pragma unroll
+    for (int q = 1; q < jqk::kMaxProblems; ++q)
+      if (q < a.nprob && i >= a.rb_begin[q]) p = q;
+    row0 = (int64_t)(i - a.rb_begin[p]) * RB;
+  };
+  auto views = [&](int p, int64_t row0, bool live, Rsrc& rc, Rsrc& rs, Rsrc& rb) {
+    const QmvProblem& pb = a.b.p[p];
+    const int64_t left = pb.N - row0;
+    const uint32_t rows = live ? (uint32_t)(left < RB ? left : RB) : 0u;
+    rc = make_rsrc((const char*)pb.codes + row0 * rowbytes, rows * rowbytes);
+    rs = make_rsrc((const char*)pb.scales + row0 * sbrow, rows * sbrow);
+    rb = make_rsrc((const char*)pb.biases + row0 * sbrow, rows * sbrow);
+  };
+  auto load_row = [&](Rsrc rc, Rsrc rs, Rsrc rb, int r, RowSlot<NW, UPL>& slot) {
+    load_chunk<NW>(rc, voff + r * rowbytes, slot.w);
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) {
+      slot.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs, vsb[t] + r * sbrow, 0, 0);
+      slot.b[t] = __builtin_amdgcn_raw_buffer_load_b16(rb, vsb[t] + r * sbrow, 0, 0);
+    }
+  };
+
+  int p;
+  int64_t row0;
+  locate(it, p, row0);
+  Rsrc rc, rs, rbv;
+  views(p, row0, true, rc, rs, rbv);
+  RowSlot<NW, UPL> ring[RB];
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
-    const int64_t row = row0 + r < N ? row0 + r : N - 1;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      load_words<BITS * UPL>(codes + row * P + (int64_t)cidx[j] * UPL * BITS, rl[r].w[j]);
-#pragma unroll
-      for (int t = 0; t < UPL; ++t) {
-        const int64_t gi = row * G + ((cidx[j] * UPL + t) >> ushift);
-        rl[r].s[j][t] = sc[gi];
-        rl[r].b[j][t] = bi[gi];
-      }
-    }
+    load_row(rc, rs, rbv, r, ring[r]);
+    // Keep the issue order row by row, as in the loop below: the wait counts at the loop
+    // head are the worse of the two orders.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
   }
 
-  XState xs[J][UPL][MT];
+  XState xs[UPL][MT];
 #pragma unroll
-  for (int j = 0; j < J; ++j)
+  for (int t = 0; t < UPL; ++t)
 #pragma unroll
-    for (int t = 0; t < UPL; ++t)
+    for (int m = 0; m < MT; ++m) {
+      jqd::XRaw& r = xr[t][m];
+      const bool live = act && m < M;
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        jqd::XRaw& r = xr[j][t][m];
-        const bool live = act[j] && m < M;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) r.d[i] = live ? r.d[i] : 0u;
-        make_xstate<D>(r, xs[j][t][m]);
-      }
-
+      for (int i = 0; i < 16; ++i) r.d[i] = live ? r.d[i] : 0u;
+      make_xstate<D>(r, xs[t][m]);
+    }
   const Bases<D> bs = jqd::make_bases<D>();
-  float acc[RB][MT];
+
+  for (int par = 0;; par ^= 1) {
+    const int nx = it + gridDim.x;
+    const bool more = nx < total;
+    int p2;
+    int64_t row02;
+    locate(more ? nx : it, p2, row02);
+    Rsrc rc2, rs2, rb2;
+    views(p2, row02, more, rc2, rs2, rb2);
+
+    float acc[RB][MT];
 #pragma unroll
-  for (int r = 0; r < RB; ++r) {
+    for (int r = 0; r < RB; ++r) {
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
-#pragma unroll
-    for (int j = 0; j < J; ++j)
+      for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
 #pragma unroll
       for (int t = 0; t < UPL; ++t) {
-        const float s = sb_to_f32<SB>(rl[r].s[j][t]);
-        const float b = sb_to_f32<SB>(rl[r].b[j][t]);
+        const float sv = sb_to_f32<SB>(ring[r].s[t]);
+        const float bv = sb_to_f32<SB>(ring[r].b[t]);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          const float d = unit_dot<D>(rl[r].w[j] + t * BITS, bs, xs[j][t][m]);
-          acc[r][m] = fmaf(s, d + xs[j][t][m].O, fmaf(b, xs[j][t][m].X, acc[r][m]));
+          const float d = unit_dot<D>(ring[r].w + t * BITS, bs, xs[t][m]);
+          acc[r][m] = fmaf(sv, d + xs[t][m].O, fmaf(bv, xs[t][m].X, acc[r][m]));
         }
       }
-  }
+      // Row r is consumed before its slot is reloaded (compiler barrier: the row's results
+      // first, then memory). The slot thus keeps its registers across the loop; a reload
+      // hoisted above the use would need a second ring and a full wait to copy it back.
+#pragma unroll
+      for (int m = 0; m < MT; ++m) asm volatile("" : "+v"(acc[r][m])::"memory");
+      load_row(rc2, rs2, rb2, r, ring[r]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 
 #pragma unroll
-  for (int r = 0; r < RB; ++r)
+    for (int r = 0; r < RB; ++r)
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[r][m] = wave_total_lane63(acc[r][m]);
-
-  void* y = pb.y;
-  if (KW == 1) {
-    if (lane == 63) {
-#pragma unroll
-      for (int r = 0; r < RB; ++r)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          const int64_t row = row0 + r;
-          if (row < N && m < M) {
-            const int64_t o = (int64_t)m * N + row;
-            if (yd == JQ_BF16) store_t<JQ_BF16>(y, o, acc[r][m]);
-            else if (yd == JQ_F16) store_t<JQ_F16>(y, o, acc[r][m]);
-            else store_t<JQ_F32>(y, o, acc[r][m]);
-          }
-        }
-    }
-  } else {
-    if (lane == 63) {
-#pragma unroll
-      for (int r = 0; r < RB; ++r)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) red[wave][r * MT + m] = acc[r][m];
-    }
+      for (int m = 0; m < MT; ++m) {
+        const float v = wave_total_lane63(acc[r][m]);
+        if (lane == 63) red[par][wave][r * MT + m] = v;
+      }
     __syncthreads();
-    const int t = threadIdx.x;
-    if (t < RB * MT) {
+    if (wave == 0 && lane < RB * MT) {
       float v = 0.f;
-      for (int w = 0; w < KW; ++w) v += red[w][t];
-      const int r = t / MT, m = t % MT;
+      for (int w = 0; w < KW; ++w) v += red[par][w][lane];
+      const int r = lane / MT, m = lane % MT;
+      const QmvProblem& pb = a.b.p[p];
       const int64_t row = row0 + r;
-      if (row < N && m < M) {
-        const int64_t o = (int64_t)m * N + row;
-        if (yd == JQ_BF16) store_t<JQ_BF16>(y, o, v);
-        else if (yd == JQ_F16) store_t<JQ_F16>(y, o, v);
-        else store_t<JQ_F32>(y, o, v);
+      if (row < pb.N && m < M) {
+        const int64_t o = (int64_t)m * pb.N + row;
+        if (a.yd == JQ_BF16) store_t<JQ_BF16>(pb.y, o, v);
+        else if (a.yd == JQ_F16) store_t<JQ_F16>(pb.y, o, v);
+        else store_t<JQ_F32>(pb.y, o, v);
       }
     }
+    if (!more) break;
+    it = nx;
+    p = p2;
+    row0 = row02;
   }
 }
 
-// Launch shape: the fewest waves per block (a power of two, at most kMaxWaves) for which
-// every lane holds one chunk of a row.
+// Grid: as many blocks as fit the GPU at once, but no more than there are row blocks, with
+// the row blocks spread evenly (every block takes the same number, up to one).
 template <class D, int SB, int MT, int RB>
-int launch_kw(const QmvBatch& b, int nprob, int64_t maxN, int ushift, int yd, hipStream_t st) {
-  constexpr int UPL = units_per_chunk<D::BITS>();
-  const int C = b.K / (32 * UPL);
-  int kw = 1;
-  while (64 * kw < C) kw *= 2;
+int launch_rb(GemvArgs& a, hipStream_t st) {
+  int kws = 0;
+  const int kw = gemv_waves(a.b.K, D::BITS, &kws);
   if (kw > kMaxWaves) return JQ_ERR_SHAPE;
-  dim3 grid((unsigned)((maxN + RB - 1) / RB), (unsigned)nprob);
-  gemv_kernel<D, SB, MT, RB, 1><<<grid, 64 * kw, 0, st>>>(b, ushift, yd);
+  a.kwshift = kws;
+  int total = 0;
+  for (int i = 0; i < a.nprob; ++i) {
+    a.rb_begin[i] = total;
+    total += (int)((a.b.p[i].N + RB - 1) / RB);
+  }
+  for (int i = a.nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
+  if (total == 0) return JQ_OK;
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_kernel<D, SB, MT, RB>, 64 * kw, 0) !=
+          hipSuccess || nb < 1)
+    nb = 1;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  const int64_t cap = (int64_t)nb * cus;
+  const int64_t iters = (total + cap - 1) / cap;
+  const int grid = (int)((total + iters - 1) / iters);
+  gemv_kernel<D, SB, MT, RB><<<grid, 64 * kw, 0, st>>>(a);
   return jqh::launch_status();
 }
 
-// Rows per block: all of a block's rows are loaded before the first is used, so RB is set by
-// the registers left after the activations (18 per unit and token).
+// Rows per block (the ring depth). Measured on MI355X: short rows (one or two waves per
+// block) do best with 4 rows, long rows (four or more waves, e.g. a 14336-wide down
+// projection) with 16; M = 4 keeps 4 rows for registers (18 per unit and token go to x).
 template <class D, int SB>
-int launch_m(const QmvBatch& b, int nprob, int64_t maxN, int ushift, int yd, hipStream_t st) {
+int launch_m(GemvArgs& a, hipStream_t st) {
   constexpr bool two = D::BITS == 2;  // two units per lane chunk
-  if (b.M == 1) return launch_kw<D, SB, 1, 8>(b, nprob, maxN, ushift, yd, st);
-  if (b.M == 2) return launch_kw<D, SB, 2, two ? 4 : 8>(b, nprob, maxN, ushift, yd, st);
-  if constexpr (!two) return launch_kw<D, SB, 4, 4>(b, nprob, maxN, ushift, yd, st);
+  const bool long_rows = gemv_waves(a.b.K, D::BITS, nullptr) >= 4;
+  if (a.b.M == 1) {
+    if (long_rows) return launch_rb<D, SB, 1, 16>(a, st);
+    return launch_rb<D, SB, 1, 4>(a, st);
+  }
+  if (a.b.M == 2) return launch_rb<D, SB, 2, 4>(a, st);
+  if constexpr (!two) return launch_rb<D, SB, 4, 4>(a, st);
   return JQ_ERR_SHAPE;
 }
 
 template <int BITS, int XDT>
-int launch_sb(const QmvBatch& b, int nprob, int64_t maxN, int ushift, int sb, int yd,
-              hipStream_t st) {
+int launch_sb(GemvArgs& a, int sb, hipStream_t st) {
   using D = Dc<BITS, 64, XDT>;  // the group size is a run-time argument of this kernel
-  if (sb == JQ_BF16) return launch_m<D, JQ_BF16>(b, nprob, maxN, ushift, yd, st);
-  return launch_m<D, JQ_F16>(b, nprob, maxN, ushift, yd, st);
+  if (sb == JQ_BF16) return launch_m<D, JQ_BF16>(a, st);
+  return launch_m<D, JQ_F16>(a, st);
 }
 
 template <int BITS>
-int launch_x(const QmvBatch& b, int nprob, int64_t maxN, int ushift, int xd, int sb, int yd,
-             hipStream_t st) {
-  if (xd == JQ_BF16) return launch_sb<BITS, JQ_BF16>(b, nprob, maxN, ushift, sb, yd, st);
-  return launch_sb<BITS, JQ_F16>(b, nprob, maxN, ushift, sb, yd, st);
+int launch_x(GemvArgs& a, int xd, int sb, hipStream_t st) {
+  if (xd == JQ_BF16) return launch_sb<BITS, JQ_BF16>(a, sb, st);
+  return launch_sb<BITS, JQ_F16>(a, sb, st);
 }
 
 }  // namespace
 
 namespace jqk {
 
-bool gemv_ok(int M, int64_t K, int bits, int gs, int xd, int sb) {
+bool gemv_ok(int M, int64_t K, int64_t maxN, int bits, int gs, int xd, int sb) {
   if (M < 1 || M > (bits == 2 ? 2 : 4)) return false;
   if (xd != JQ_BF16 && xd != JQ_F16) return false;
   if (sb != JQ_BF16 && sb != JQ_F16) return false;
   const int64_t chunk = bits == 2 ? 64 : 32;  // K of one lane chunk
-  if (K <= 0 || K % chunk || K / chunk > 64 * kMaxWaves) return false;
-  (void)gs;
-  return true;
+  if (K <= 0 || K % chunk || gemv_waves(K, bits, nullptr) > kMaxWaves) return false;
+  // Byte offsets inside a row block's buffer views stay far below 2^31.
+  return (maxN + 64) * (K / gs) * 2 < ((int64_t)1 << 31) && K * bits / 8 < ((int64_t)1 << 24);
 }
 
 int gemv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
@@ -346,15 +421,31 @@ int gemv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, 
   int64_t maxN = 0;
   for (int i = 0; i < nprob; ++i) maxN = b.p[i].N > maxN ? b.p[i].N : maxN;
   if (maxN == 0 || b.M == 0) return JQ_OK;
-  if (!gemv_ok(b.M, b.K, bits, gs, xd, sb)) return JQ_ERR_SHAPE;
-  const int us = gs == 32 ? 0 : gs == 64 ? 1 : 2;
+  if (!gemv_ok(b.M, b.K, maxN, bits, gs, xd, sb)) return JQ_ERR_SHAPE;
+  // Problems of one launch must share the activations (x stays in registers).
+  for (int i = 1; i < nprob; ++i) {
+    if (b.p[i].x != b.p[0].x) {
+      for (int j = 0; j < nprob; ++j) {
+        QmvBatch one = b;
+        one.p[0] = b.p[j];
+        const int s = gemv_launch(one, 1, bits, gs, xd, sb, yd, st);
+        if (s) return s;
+      }
+      return JQ_OK;
+    }
+  }
+  GemvArgs a;
+  a.b = b;
+  a.nprob = nprob;
+  a.ushift = gs == 32 ? 0 : gs == 64 ? 1 : 2;
+  a.yd = yd;
   switch (bits) {
-    case 2: return launch_x<2>(b, nprob, maxN, us, xd, sb, yd, st);
-    case 3: return launch_x<3>(b, nprob, maxN, us, xd, sb, yd, st);
-    case 4: return launch_x<4>(b, nprob, maxN, us, xd, sb, yd, st);
-    case 5: return launch_x<5>(b, nprob, maxN, us, xd, sb, yd, st);
-    case 6: return launch_x<6>(b, nprob, maxN, us, xd, sb, yd, st);
-    default: return launch_x<8>(b, nprob, maxN, us, xd, sb, yd, st);
+    case 2: return launch_x<2>(a, xd, sb, st);
+    case 3: return launch_x<3>(a, xd, sb, st);
+    case 4: return launch_x<4>(a, xd, sb, st);
+    case 5: return launch_x<5>(a, xd, sb, st);
+    case 6: return launch_x<6>(a, xd, sb, st);
+    default: return launch_x<8>(a, xd, sb, st);
   }
 }
 

@@ -28,7 +28,7 @@ int qmv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, i
                hipStream_t st);
 
 // Decode GEMV on the vector ALUs (jq_gemv.hip): M <= 4, bf16/f16 activations and scales.
-bool gemv_ok(int M, int64_t K, int bits, int gs, int xd, int sb);
+bool gemv_ok(int M, int64_t K, int64_t maxN, int bits, int gs, int xd, int sb);
 int gemv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
                 hipStream_t st);
 

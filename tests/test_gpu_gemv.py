@@ -46,10 +46,18 @@ def test_gemv_output_dtypes(ydt):
 
 def test_gemv_fallback_shapes():
     """Shapes outside the kernel's range go to the other kernels: 2-bit K % 64 != 0,
-    K beyond 512 chunks, 2-bit M = 3."""
+    K beyond 512 chunks, 2-bit M = 3, groups per row not a multiple of 8."""
     run_case(1, 16, 96, 2, 32, seed=1)
     run_case(1, 16, 16384 + 64, 3, 64, seed=2)
     run_case(3, 16, 512, 2, 64, seed=3)
+    run_case(1, 21, 64 * 12, 3, 64, seed=4)
+
+
+@pytest.mark.parametrize("N", [1, 7, 8, 9, 17, 33])
+def test_gemv_row_tails(N):
+    """Row blocks cut by the end of the matrix (scales window ends exactly at the view)."""
+    run_case(1, N, 512, 4, 64, seed=N)
+    run_case(2, N, 1024, 3, 128, seed=N + 1)
 
 
 def test_gemv_grouped_launch():
