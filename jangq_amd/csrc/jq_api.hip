@@ -6,6 +6,9 @@
 
 namespace {
 
+// Activation rows from which the 256 x 256-tile prefill GEMM takes over.
+constexpr int64_t kGemmMinRows = 64;
+
 int dense_one(const void* x, int xd, const uint32_t* codes, const void* scales,
               const void* biases, int sb, int bits, int gs, int64_t M, int64_t N, int64_t K,
               void* y, int yd, hipStream_t st) {
@@ -26,6 +29,14 @@ int dense_one(const void* x, int xd, const uint32_t* codes, const void* scales,
     b.p[0].x = x; b.p[0].codes = codes; b.p[0].scales = scales; b.p[0].biases = biases;
     b.p[0].y = y; b.p[0].N = N;
     return jqk::dec_dense_launch(b, 1, bits, gs, xd, sb, yd, st);
+  }
+  if (M >= kGemmMinRows && jqk::gemm_ok(M, K, bits, gs, xd, sb)) {
+    jqk::QmmProblem p;
+    p.x = x; p.codes = codes; p.scales = scales; p.biases = biases; p.y = y;
+    p.M = M; p.N = N; p.K = K;
+    p.expert_stride_codes = 0;
+    p.expert_stride_sb = 0;
+    return jqk::gemm_launch(p, bits, gs, xd, sb, yd, st);
   }
   if (M > 4 && mfma_ok) {
     jqk::QmmProblem p;

@@ -32,6 +32,10 @@ bool gemv_ok(int M, int64_t K, int64_t maxN, int bits, int gs, int xd, int sb);
 int gemv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
                 hipStream_t st);
 
+// Prefill GEMM on the matrix cores (jq_gemm.hip): gs 64/128, bf16/f16 activations
+// (8-bit codes only with f16 activations).
+bool gemm_ok(int64_t M, int64_t K, int bits, int gs, int xd, int sb);
+
 // Row-gathered operand description for the grouped (MoE) matrix-core launches.
 // Pairs are processed in expert-grouped order `order`; A row r of segment e is
 //   pair p = order[seg_off[e] + r / M], token row m = r % M
@@ -61,6 +65,7 @@ struct QmmProblem {
 
 // Matrix-core GEMM y = x @ deq(W)^T. K % 128 == 0 required. Returns a jq_status.
 int qmm_launch(const QmmProblem& p, int bits, int gs, int xd, int sb, int yd, hipStream_t st);
+int gemm_launch(const QmmProblem& p, int bits, int gs, int xd, int sb, int yd, hipStream_t st);
 
 // Grouped matrix-core GEMM over expert segments described by `plan` (device data). With
 // p2 != NULL, p is the gate and p2 the up projection (same shapes) and the output is

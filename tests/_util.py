@@ -70,10 +70,31 @@ class QWeight:
         return O.dequantize_affine(self.packed, self.s, self.b, self.bits, self.gs)
 
 
+def half_ulp(v: np.ndarray, dtype: str) -> np.ndarray:
+    """Half a unit in the last place of |v| in a 16-bit float format (0 for fp32): the
+    rounding every correctly rounded output of that dtype may carry."""
+    if dtype not in ("bf16", "f16"):
+        return np.zeros_like(np.asarray(v, dtype=np.float64))
+    mant = 8 if dtype == "bf16" else 11
+    e = np.floor(np.log2(np.maximum(np.abs(np.asarray(v, dtype=np.float64)), 1e-30)))
+    if dtype == "f16":
+        e = np.maximum(e, -14)
+    return np.ldexp(1.0, (e - mant).astype(np.int64))
+
+
 def assert_close(got: np.ndarray, ref: np.ndarray, what: str,
-                 rel=REL_L2_TOL, mabs=MAX_ABS_TOL):
+                 rel=REL_L2_TOL, mabs=MAX_ABS_TOL, exact=None, out_dtype=None):
+    """rel-L2 of got against ref (the reference rounded to the output dtype) and max-abs
+    error. With `exact` (the unrounded fp32/fp64 accumulation) the max-abs bound applies to
+    |got - exact| beyond the output rounding itself (half an ulp of out_dtype): an output
+    that rounds the other way at a rounding boundary is then not charged a full ulp."""
     r = O.rel_l2(got, ref)
-    m = O.max_abs(got, ref)
+    if exact is None:
+        m = O.max_abs(got, ref)
+    else:
+        dev = np.abs(np.asarray(got, np.float64) - np.asarray(exact, np.float64))
+        m = float(np.max(dev - half_ulp(exact, out_dtype))) if dev.size else 0.0
+        m = max(m, 0.0)
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
     assert r <= rel and m <= mabs, f"{what}: rel_l2={r:.3e} (tol {rel}) max_abs={m:.3e} (tol {mabs})"
     return r, m

@@ -1,0 +1,66 @@
+"""GPU parity of the prefill matrix-core GEMM (large M) against the oracle.
+
+Covers ragged M and N against the 256 x 256 block tile, K with one or several 16-group
+batches of the bias term (and a partial last batch), group sizes 64 and 128, every width on
+bf16 and f16 activations, and groups whose scale is zero (or tiny): those run with s = 1 and
+codes 0 and must still give b * sum(x). Tolerances: rel-L2 <= 1e-3 and max-abs <= 2e-2 after
+rounding to the output dtype; fp32 outputs rel-L2 <= 1e-4 (the bias term goes through the
+matrix cores as bf16 high/low parts, about 2^-17 relative)."""
+import numpy as np
+import pytest
+import torch
+
+import jangq_amd as jq
+from oracle import jangq_oracle as O
+from tests._util import QWeight, assert_close, to_tensor, values_of
+from tests.test_gpu_matmul import run_case
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 256, 256), (100, 200, 1024), (256, 513, 2048),
+                                   (300, 256, 64 * 17), (513, 96, 512)])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6])
+def test_gemm_shapes_bits(M, N, K, bits):
+    run_case(M, N, K, bits, 64, seed=M + N + bits)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 6, 8])
+@pytest.mark.parametrize("gs", [64, 128])
+def test_gemm_f16_and_group_sizes(bits, gs):
+    run_case(130, 160, 128 * 9, bits, gs, xdt="f16", sidecar="f16", seed=bits + gs)
+    if bits != 8:
+        run_case(130, 160, 128 * 9, bits, gs, seed=bits + gs + 1)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 6])
+def test_gemm_fp32_output(bits):
+    M, N, K, gs = 256, 256, 1024, 64
+    qw = QWeight(N, K, bits, gs, seed=7)
+    rng = np.random.default_rng(8)
+    x = O.round_bf16(rng.standard_normal((M, K), dtype=np.float32))
+    y = jq.quantized_matmul(to_tensor(x, "bf16"), qw.dw, qw.ds, qw.db, True, gs, bits,
+                            out=torch.empty((M, N), dtype=torch.float32, device="cuda"))
+    ref = O.quantized_matmul(x, qw.packed, qw.s, qw.b, bits, gs)
+    assert_close(values_of(y), ref, f"fp32 out b{bits}", rel=1e-4, mabs=2e-3)
+
+
+@pytest.mark.parametrize("scale", [0.0, 1e-35])
+def test_gemm_zero_scale_groups(scale):
+    """Groups with scale 0 (or below 2^-100) contribute b * sum(x) exactly."""
+    M, N, K, bits, gs = 96, 64, 512, 4, 64
+    qw = QWeight(N, K, bits, gs, seed=3)
+    s = qw.s.copy()
+    s[::3, 1::2] = scale  # every third row: odd groups
+    s_t = torch.from_numpy(O.f32_to_bf16_bits(s).view(np.int16)).view(torch.bfloat16).cuda()
+    rng = np.random.default_rng(4)
+    x = O.round_bf16(rng.standard_normal((M, K), dtype=np.float32))
+    y = jq.quantized_matmul(to_tensor(x, "bf16"), qw.dw, s_t, qw.db, True, gs, bits)
+    ref = O.quantized_matmul(x, qw.packed, O.round_bf16(s), qw.b, bits, gs)
+    assert_close(values_of(y), O.round_bf16(ref), "zero-scale groups", exact=ref, out_dtype="bf16")
+
+
+def test_gemm_c4_shape_slice():
+    """Config-4 geometry (K = 4096, N = 14336) on a 256-row slice, 4- and 3-bit."""
+    for bits in (4, 3):
+        run_case(256, 14336, 4096, bits, 64, seed=400 + bits)

@@ -315,3 +315,14 @@ def test_route_topk_vs_full_sort():
         assert idx[t].tolist() == order
         np.testing.assert_allclose(w[t], p[order] / p[order].sum(), rtol=1e-12)
     assert idx[0, 0] == 5 and idx[0, 1] == 9
+
+
+def test_half_ulp_helper():
+    """The test helper's rounding allowance: half an ulp of bf16 / f16 at |v|."""
+    from tests._util import half_ulp
+    v = np.array([1.0, 1.99, 2.0, -3.0, 6.8, 0.0], dtype=np.float32)
+    assert np.array_equal(half_ulp(v, "bf16"), [2**-8, 2**-8, 2**-7, 2**-7, 2**-6, 2**-108])
+    assert np.array_equal(half_ulp(np.array([1.0, 1e-6]), "f16"), [2**-11, 2**-25])
+    # a bf16 rounding of any value stays within the allowance
+    r = np.random.default_rng(0).standard_normal(1000).astype(np.float32) * 50
+    assert np.all(np.abs(O.round_bf16(r) - r) <= half_ulp(r, "bf16"))
