@@ -147,8 +147,11 @@ struct Magic {
 };
 
 // Four magic pairs of an 8-code chunk whose 8*BITS bits sit at the bottom of (v_hi:v).
+// `base` is Magic<FMT, BITS>::base; callers that keep it in a register get one v_and_or_b32
+// per pair (gfx9 VOP3 forms take no literal operand).
 template <int FMT, int BITS>
-JQ_DEV void chunk_to_pairs(uint32_t v, uint32_t v_hi, uint32_t out[4]) {
+JQ_DEV void chunk_to_pairs(uint32_t v, uint32_t v_hi, uint32_t out[4],
+                           uint32_t base = Magic<FMT, BITS>::base) {
   using Mg = Magic<FMT, BITS>;
   constexpr uint32_t m = (1u << BITS) - 1u;
   constexpr int sh = Mg::shift;
@@ -162,7 +165,7 @@ JQ_DEV void chunk_to_pairs(uint32_t v, uint32_t v_hi, uint32_t out[4]) {
     for (int p = 0; p < 4; ++p) {
       const int s = p * BITS - sh;
       const uint32_t t = s >= 0 ? (u >> s) : (u << (-s));
-      out[p] = (t & (fm | (fm << 16))) | Mg::base;
+      out[p] = (t & (fm | (fm << 16))) | base;
     }
   } else {
     constexpr int half = 4 * BITS;  // 20, 24 or 32 bits
@@ -174,20 +177,21 @@ JQ_DEV void chunk_to_pairs(uint32_t v, uint32_t v_hi, uint32_t out[4]) {
       const int s = p * BITS - sh;
       const uint32_t a = s >= 0 ? (lo >> s) : (lo << (-s));
       const uint32_t b = s >= 0 ? (hi >> s) : (hi << (-s));
-      out[p] = (a & fm) | ((b & fm) << 16) | Mg::base;
+      out[p] = (a & fm) | ((b & fm) << 16) | base;
     }
   }
 }
 
 // Chunk c (0..3) of a unit (32 codes in BITS words): bits [8*BITS*c, 8*BITS*(c+1)).
 template <int FMT, int BITS, int C>
-JQ_DEV void unit_chunk_pairs(const uint32_t* w, uint32_t out[4]) {
+JQ_DEV void unit_chunk_pairs(const uint32_t* w, uint32_t out[4],
+                             uint32_t base = Magic<FMT, BITS>::base) {
   constexpr int off = 8 * BITS * C;
   constexpr int len = 8 * BITS;
   if constexpr (len <= 32) {
-    chunk_to_pairs<FMT, BITS>(field<off, len>(w), 0u, out);
+    chunk_to_pairs<FMT, BITS>(field<off, len>(w), 0u, out, base);
   } else {
-    chunk_to_pairs<FMT, BITS>(field<off, 32>(w), field<off + 32, len - 32>(w), out);
+    chunk_to_pairs<FMT, BITS>(field<off, 32>(w), field<off + 32, len - 32>(w), out, base);
   }
 }
 

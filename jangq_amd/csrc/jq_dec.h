@@ -145,6 +145,10 @@ JQ_DEV Bases<D> make_bases() {
         r.v[i] = r.v[base_rep<D::BITS>(i)];
       }
     }
+  } else if constexpr (!D::NIB) {
+    // The single magic base of the unscheduled forms, also pinned in a register.
+    r.v[0] = Magic<D::XDT, D::BITS>::base;
+    asm volatile("" : "+v"(r.v[0]));
   }
   return r;
 }
@@ -189,13 +193,13 @@ JQ_DEV void b_frag(const uint32_t* w, const Bases<D>& bs, u32x4& b, u32x4& bh) {
       const int j = 4 * (F & 1) + p;
       const int s = 2 * j - sh;
       const uint32_t t = s >= 0 ? (word >> s) : (word << (-s));
-      o[p] = (t & pm) | Mg::base;
+      o[p] = (t & pm) | bs.v[0];
     }
     b = u32x4{o[0], o[1], o[2], o[3]};
     bh = b;
   } else {
     uint32_t o[4];
-    unit_chunk_pairs<D::XDT, D::BITS, F>(w, o);
+    unit_chunk_pairs<D::XDT, D::BITS, F>(w, o, bs.v[0]);
     b = u32x4{o[0], o[1], o[2], o[3]};
     bh = b;
   }

@@ -20,7 +20,7 @@
 // tiles of v_mfma_f32_32x32x16). K advances in stages of 32 (one 32-code unit per row of W):
 // waves 0-3 stage the activations (one row each: permute into the code order of the unit,
 // partial X), waves 4-7 the codes (one column each: unpack to magic values, scales at group
-// starts); both write double-buffered LDS, one barrier per stage, global loads four stages
+// starts); both write double-buffered LDS, one barrier per stage, global loads two stages
 // ahead in a register ring.
 // MFMA operand mapping: lane half h of k-step t takes unit fragment F = 2h + t (8 codes), for
 // A and B alike, so the fragment order inside a unit cancels.
@@ -134,13 +134,13 @@ __global__ void __launch_bounds__(NTH, 1) gemm_kernel(GemmArgs a) {
   const int64_t arow = m0 + sr, bcol = n0 + sr;
   const bool alive = arow < a.M, blive = bcol < a.N;
 
-  // Prefetch ring: the loads of stage k land in slot k % 4, four stages ahead of use.
+  // Prefetch ring: the loads of stage k land in slot k % 2, two stages ahead of use.
   struct Slot {
     u32x4 x[2];      // 16 activations of the row half
     uint32_t w[BITS];  // the column's unit (both halves load it)
     uint32_t s, b;   // raw scale and bias of the stage's group
   };
-  Slot pf[4];
+  Slot pf[2];
   uint32_t zmask = ~0u;
   float sprev = 1.f, xg = 0.f;
 
@@ -204,7 +204,7 @@ __global__ void __launch_bounds__(NTH, 1) gemm_kernel(GemmArgs a) {
     float u = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) u = dot2<D::XDT>(xr.d[i], D::ONE2, u);
-    u += __shfl_xor(u, 1, 64);
+    u += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, u), 0xB1, 0xF, 0xF, false));  // + partner half (lane ^ 1)
     xg = gfirst ? u : xg + u;
     if constexpr (glast) {
       // X of the group as 16-bit high and low parts into its batch slot.
@@ -223,7 +223,7 @@ __global__ void __launch_bounds__(NTH, 1) gemm_kernel(GemmArgs a) {
       const bool zero = fabsf(sv) < 7.8886091e-31f;  // NaN keeps its scale
       const float sp = !zero ? sv : g > 0 ? sprev : fmaxf(fabsf(bv), 8.6736174e-19f) / D::OFF;
       zmask = zero || !blive ? 0u : ~0u;
-      sm.r[buf][sr] = sprev / sp;
+      sm.r[buf][sr] = sprev * __builtin_amdgcn_rcpf(sp);  // ratio to ~1 ulp
       sm.cb[sr][gb] = blive ? fmaf(-D::OFF, sp, bv) : 0.f;
       sm.sl[sr] = sp;  // the last group's value remains
       sprev = sp;
@@ -310,27 +310,27 @@ __global__ void __launch_bounds__(NTH, 1) gemm_kernel(GemmArgs a) {
   };
 
   // Pipeline: stage k+1 is written to LDS while stage k is multiplied; its loads were issued
-  // four stages earlier into ring slot (k+1) % 4. The loop runs 4 stages per trip so that
+  // two stages earlier into ring slot (k+1) % 2. The loop runs 4 stages per trip so that
   // slots and in-group positions are compile-time.
   using I0 = std::integral_constant<int, 0>;
   load_stage(0, pf[0]);
-  if (S > 1) load_stage(1, pf[1]);
-  if (S > 2) load_stage(2, pf[2]);
-  if (S > 3) load_stage(3, pf[3]);
+  load_stage(S > 1 ? 1 : S - 1, pf[1]);
   stage(0, pf[0], I0{});
   __syncthreads();
-  if (S > 4) load_stage(4, pf[0]);
+  load_stage(S > 2 ? 2 : S - 1, pf[0]);
+  // One step: the MFMAs of stage k, the staging of stage k+1, the rare batch work.
   auto step = [&](int k, auto j_c) {
     constexpr int J = decltype(j_c)::value;
     constexpr int KIN = J % SPG, NKIN = (J + 1) % SPG;
     compute(k, std::integral_constant<int, KIN>{});
+    if (k + 1 < S) stage(k + 1, pf[(J + 1) & 1], std::integral_constant<int, NKIN>{});
     if (KIN == SPG - 1) {
       const int g = k / SPG;
       if ((g % BATCH) == BATCH - 1 || g == G - 1) batch_mfma();
     }
-    if (k + 1 < S) stage(k + 1, pf[(J + 1) & 3], std::integral_constant<int, NKIN>{});
     __syncthreads();
-    if (k + 5 < S) load_stage(k + 5, pf[(J + 1) & 3]);
+    // Past the last stage the slot is refilled with stage S-1 again and never staged.
+    load_stage(k + 3 < S ? k + 3 : S - 1, pf[(J + 1) & 1]);
   };
   for (int k0 = 0; k0 < S; k0 += 4) {
     step(k0, I0{});

@@ -18,8 +18,8 @@ from tests.test_gpu_matmul import run_case
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 256, 256), (100, 200, 1024), (256, 513, 2048),
-                                   (300, 256, 64 * 17), (513, 96, 512)])
+@pytest.mark.parametrize("M,N,K", [(384, 256, 256), (400, 200, 1024), (520, 513, 2048),
+                                   (600, 256, 64 * 17), (513, 96, 512)])
 @pytest.mark.parametrize("bits", [2, 3, 4, 5, 6])
 def test_gemm_shapes_bits(M, N, K, bits):
     run_case(M, N, K, bits, 64, seed=M + N + bits)
@@ -28,14 +28,14 @@ def test_gemm_shapes_bits(M, N, K, bits):
 @pytest.mark.parametrize("bits", [2, 3, 4, 6, 8])
 @pytest.mark.parametrize("gs", [64, 128])
 def test_gemm_f16_and_group_sizes(bits, gs):
-    run_case(130, 160, 128 * 9, bits, gs, xdt="f16", sidecar="f16", seed=bits + gs)
+    run_case(390, 160, 128 * 9, bits, gs, xdt="f16", sidecar="f16", seed=bits + gs)
     if bits != 8:
-        run_case(130, 160, 128 * 9, bits, gs, seed=bits + gs + 1)
+        run_case(390, 160, 128 * 9, bits, gs, seed=bits + gs + 1)
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4, 6])
 def test_gemm_fp32_output(bits):
-    M, N, K, gs = 256, 256, 1024, 64
+    M, N, K, gs = 384, 256, 1024, 64
     qw = QWeight(N, K, bits, gs, seed=7)
     rng = np.random.default_rng(8)
     x = O.round_bf16(rng.standard_normal((M, K), dtype=np.float32))
@@ -48,7 +48,7 @@ def test_gemm_fp32_output(bits):
 @pytest.mark.parametrize("scale", [0.0, 1e-35])
 def test_gemm_zero_scale_groups(scale):
     """Groups with scale 0 (or below 2^-100) contribute b * sum(x) exactly."""
-    M, N, K, bits, gs = 96, 64, 512, 4, 64
+    M, N, K, bits, gs = 400, 64, 512, 4, 64
     qw = QWeight(N, K, bits, gs, seed=3)
     s = qw.s.copy()
     s[::3, 1::2] = scale  # every third row: odd groups
@@ -61,6 +61,6 @@ def test_gemm_zero_scale_groups(scale):
 
 
 def test_gemm_c4_shape_slice():
-    """Config-4 geometry (K = 4096, N = 14336) on a 256-row slice, 4- and 3-bit."""
+    """Config-4 geometry (K = 4096, N = 14336) on a 512-row slice, 4- and 3-bit."""
     for bits in (4, 3):
-        run_case(256, 14336, 4096, bits, 64, seed=400 + bits)
+        run_case(512, 14336, 4096, bits, 64, seed=400 + bits)
