@@ -242,7 +242,13 @@ def bench_moe(gen, name, E, H, I, bits, gs, k, T, steps, warmup, shared_I=None, 
             perm = torch.randperm(E, generator=gen, device="cuda")[: round(0.1 * E)]
             lg[:, perm] += 2.0
         logit_sets.append(lg)
-    ms = timed(lambda i: blk(xs[i % R], logits=logit_sets[i % R]), steps, warmup)
+    def step(i):
+        # The router GEMV runs (its bytes are counted below); routing uses the config's
+        # synthetic N(0,1) logits so that the expert load is the one the config states.
+        blk.gate(xs[i % R])
+        return blk(xs[i % R], logits=logit_sets[i % R])
+
+    ms = timed(step, steps, warmup)
     # Algorithmic bytes of one layer: router + distinct selected experts (+ shared).
     per_expert = 3 * (I * H * bits // 8 + I * (H // gs) * 4)  # gate + up + down
     distinct = []

@@ -23,136 +23,15 @@
 // i.e. the reference's  s * sum q x + b * sum x  (jang-tools/jang_tools/dsv41/metal_decode.py:202-233).
 // Accumulation is fp32. Each (row, token) partial is summed over the wave with DPP row
 // operations and over the block's waves through LDS.
-#include "jq_dec.h"
+#include "jq_gemv.h"
 #include "jq_qmv.h"
 
 namespace {
 
 using namespace jq;
-using jqd::Bases;
-using jqd::Dc;
+using namespace jqg;
 using jqk::QmvBatch;
 using jqk::QmvProblem;
-
-template <int BITS>
-constexpr int units_per_chunk() {
-  return BITS == 2 ? 2 : 1;
-}
-
-// Activation state of one unit for one token: the 16 activation dwords paired as the unit's
-// code dwords, X = sum x, O = -sum offset_k x_k.
-struct XState {
-  uint32_t pr[16];
-  float X, O;
-};
-
-template <class D, int F, int P>
-JQ_DEV uint32_t xpair_of(const jqd::XRaw& r) {
-  return jqd::xpair<jqd::code_lo<D>(F, P), jqd::code_hi<D>(F, P)>(r);
-}
-
-template <class D>
-JQ_DEV void make_xstate(const jqd::XRaw& r, XState& xs) {
-#define JQ_XP(F, P) xs.pr[4 * F + P] = xpair_of<D, F, P>(r);
-  JQ_XP(0, 0) JQ_XP(0, 1) JQ_XP(0, 2) JQ_XP(0, 3)
-  JQ_XP(1, 0) JQ_XP(1, 1) JQ_XP(1, 2) JQ_XP(1, 3)
-  JQ_XP(2, 0) JQ_XP(2, 1) JQ_XP(2, 2) JQ_XP(2, 3)
-  JQ_XP(3, 0) JQ_XP(3, 1) JQ_XP(3, 2) JQ_XP(3, 3)
-#undef JQ_XP
-  float X = 0.f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) X = dot2<D::XDT>(r.d[i], D::ONE2, X);
-  xs.X = X;
-  if constexpr (D::SCHED) {
-    float O = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) O = dot2<D::XDT>(jqd::bo_dword<D>(i >> 2, i & 3), xs.pr[i], O);
-    xs.O = O;
-  } else if constexpr (D::NIB) {
-    xs.O = -272.f * X;
-  } else {
-    xs.O = -(float)(1 << D::BITS) * X;
-  }
-}
-
-// Dot product of one unit's exact code values with its paired activations.
-template <class D>
-JQ_DEV float unit_dot(const uint32_t* w, const Bases<D>& bs, const XState& xs) {
-  float d0 = 0.f, d1 = 0.f;
-#define JQ_UF(F)                                                          \
-  {                                                                       \
-    u32x4 b, bh;                                                          \
-    jqd::b_frag<D, F>(w, bs, b, bh);                                      \
-    d0 = dot2<D::XDT>(b[0], xs.pr[4 * F + 0], d0);                        \
-    d0 = dot2<D::XDT>(b[1], xs.pr[4 * F + 1], d0);                        \
-    d0 = dot2<D::XDT>(b[2], xs.pr[4 * F + 2], d0);                        \
-    d0 = dot2<D::XDT>(b[3], xs.pr[4 * F + 3], d0);                        \
-    if constexpr (D::NIB) {                                               \
-      d1 = dot2<D::XDT>(bh[0], xs.pr[4 * F + 0], d1);                     \
-      d1 = dot2<D::XDT>(bh[1], xs.pr[4 * F + 1], d1);                     \
-      d1 = dot2<D::XDT>(bh[2], xs.pr[4 * F + 2], d1);                     \
-      d1 = dot2<D::XDT>(bh[3], xs.pr[4 * F + 3], d1);                     \
-    }                                                                     \
-  }
-  JQ_UF(0) JQ_UF(1) JQ_UF(2) JQ_UF(3)
-#undef JQ_UF
-  if constexpr (D::NIB) return fmaf(16.f, d1, d0);
-  return d0;
-}
-
-// Sum over the 64 lanes with DPP row operations; the total lands in lane 63.
-JQ_DEV float wave_total_lane63(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false)); // row_ror 4
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false)); // row_ror 8
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false)); // row_bcast 15
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false)); // row_bcast 31
-  return v;
-}
-
-template <int SB>
-JQ_DEV float sb_to_f32(uint32_t h) {
-  if constexpr (SB == JQ_BF16) return __uint_as_float(h << 16);
-  else return f16_bits_to_f32((uint16_t)h);
-}
-
-typedef __amdgpu_buffer_rsrc_t Rsrc;
-typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-// Raw buffer view of `bytes` bytes at p: loads past the end read zero and touch no memory.
-JQ_DEV Rsrc make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-
-// The BITS*UPL code words of a lane chunk at byte voff of a row block. All offsets go into
-// the vector offset: the buffer range check covers it, not the scalar offset.
-template <int NW>
-JQ_DEV void load_chunk(Rsrc r, uint32_t voff, uint32_t* w) {
-  constexpr int soff = 0;
-  if constexpr (NW == 4) {
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-    w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
-  } else if constexpr (NW == 8) {
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-    const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
-    w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
-    w[4] = u[0]; w[5] = u[1]; w[6] = u[2]; w[7] = u[3];
-  } else if constexpr (NW == 3) {
-    const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, 0);
-    w[0] = v[0]; w[1] = v[1]; w[2] = v[2];
-  } else if constexpr (NW == 6) {
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, voff + 8 * i, soff, 0);
-      w[2 * i] = v[0]; w[2 * i + 1] = v[1];
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < NW; ++i) w[i] = __builtin_amdgcn_raw_buffer_load_b32(r, voff + 4 * i, soff, 0);
-  }
-}
 
 // Launch arguments: problems of one grouped launch share x, M, K and the dtypes; their row
 // blocks are numbered 0 .. rb_begin[nprob) in problem order.
@@ -163,27 +42,6 @@ struct GemvArgs {
   int ushift;    // log2(gs / 32)
   int kwshift;   // log2(waves per block)
   int yd;
-};
-
-// Block = KW waves (blockDim.x = 64 * KW, KW <= kMaxWaves).
-constexpr int kMaxWaves = 8;
-
-// Waves per block for a K: the fewest (a power of two) for which each lane holds one chunk.
-inline int gemv_waves(int64_t K, int bits, int* shift) {
-  const int upl = bits == 2 ? 2 : 1;
-  const int64_t C = K / (32 * upl);
-  int kw = 1, ks = 0;
-  while (64 * kw < C) kw *= 2, ++ks;
-  if (shift) *shift = ks;
-  return kw;
-}
-
-// One row of a lane's ring slot: the chunk's code words, and the scale and bias of each of
-// its units (units of one group load the same element).
-template <int NW, int UPL>
-struct RowSlot {
-  uint32_t w[NW];
-  uint32_t s[UPL], b[UPL];
 };
 
 // Persistent: block b handles row blocks b, b + gridDim.x, ... Each lane keeps a rolling

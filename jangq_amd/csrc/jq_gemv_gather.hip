@@ -1,0 +1,348 @@
+// Expert-gathered decode GEMV on the vector ALUs: the MoE gather_qmm and SwitchGLU launches
+// when each selected expert serves only a few activation rows (decode batches).
+//
+//   y[o(r), n] = sum_k x[i(r), k] * (q_e[n,k] * s_e[n,k/gs] + b_e[n,k/gs])
+//
+// for every row r of the expert-grouped plan (expert e, x row i(r), output row o(r)), and with
+// two projections (gate, up) of the same expert:  h = silu(gate) * up.
+//
+// Work items are (tile, row block): a tile is up to MT plan rows of one expert, a row block
+// RB / NB consecutive weight rows of that expert (NB = 2: each row of gate and of up). The
+// kernel reads the number of tiles from the plan, numbers the items tile-major and gives each
+// block one contiguous range, so a block changes tiles rarely. Inside a block the arithmetic
+// and the register ring are those of the dense GEMV: a lane holds its K slice of the tile's
+// activation rows, the ring holds the next item's rows in flight while the block computes,
+// reduces and stores the current one. At a tile change the block reloads the activations.
+//
+// Reference: gather_qmm over affine codes (mlx.core.gather_qmm as called from
+// jang-tools/jang_tools/dots3/ops.py:202-214 and jangrt/switchglu_decode.py:161-183), the
+// per-group affine sum s * sum q x + b * sum x (jang-tools/jang_tools/dsv41/metal_decode.py:202-233).
+#include "jq_gemv.h"
+#include "jq_qmv.h"
+
+namespace {
+
+using namespace jq;
+using namespace jqg;
+using jqk::GatherPlan;
+using jqk::QmmProblem;
+
+struct GatherArgs {
+  QmmProblem p[2];  // the projection (and up, NB == 2); output and shapes from p[0]
+  GatherPlan plan;
+  int nrb;          // row blocks per tile
+  int ushift;       // log2(gs / 32)
+  int kwshift;      // log2(waves per block)
+  int yd;
+};
+
+JQ_DEV float round_out(float v, int yd) {
+  if (yd == JQ_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  if (yd == JQ_F16) return f16_bits_to_f32(f32_to_f16_bits(v));
+  return v;
+}
+
+JQ_DEV void store_out(void* y, int64_t i, float v, int yd) {
+  if (yd == JQ_BF16) store_t<JQ_BF16>(y, i, v);
+  else if (yd == JQ_F16) store_t<JQ_F16>(y, i, v);
+  else store_t<JQ_F32>(y, i, v);
+}
+
+// The activation and output rows of a tile's MT plan rows (wave-uniform). A plan row past
+// the tile, or whose x row lies outside x, reads zeros; only rows inside the tile are stored.
+template <int MT>
+struct TileRows {
+  int64_t xrow[MT];
+  int64_t orow[MT];
+  bool xlive[MT];
+  int nrows;
+};
+
+template <int MT>
+JQ_DEV void tile_rows(const GatherPlan& pl, int4 tl, TileRows<MT>& tr) {
+  tr.nrows = tl.z;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const int rr = tl.y + (m < tl.z ? m : 0);
+    const int Mp = pl.M;
+    const int pi = Mp == 1 ? rr : rr / Mp, mi = Mp == 1 ? 0 : rr - pi * Mp;
+    const uint32_t pair = pl.order[tl.w + pi];
+    const int64_t xr = (int64_t)(pl.lhs ? pl.lhs[pair] : pair / (uint32_t)pl.pair_div) * Mp + mi;
+    tr.xlive[m] = m < tl.z && xr < pl.x_rows;
+    tr.xrow[m] = tr.xlive[m] ? xr : 0;
+    tr.orow[m] = (int64_t)pair * Mp + mi;
+  }
+}
+
+template <class D, int SB, int MT, int RB, int NB>
+__global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs a) {
+  constexpr int BITS = D::BITS;
+  constexpr int UPL = units_per_chunk<BITS>();
+  constexpr int NW = BITS * UPL;
+  constexpr int ROWS = RB / NB;  // weight rows of one projection per item
+  __shared__ float red[2][kMaxWaves][RB * MT];
+
+  const int items = *a.plan.n_tiles * a.nrb;
+  const int per = (items + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int first = blockIdx.x * per;
+  const int end = first + per < items ? first + per : items;
+  if (first >= end) return;  // whole block
+  const int KW = blockDim.x >> 6;
+  const int K = (int)a.p[0].K;
+  const int64_t N = a.p[0].N;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int C = K / (32 * UPL);                       // chunks per row
+  const int CW = (C + KW - 1) >> a.kwshift;           // chunks per wave
+  const uint32_t rowbytes = (uint32_t)(K / 32) * BITS * 4;
+  const uint32_t sbrow = (uint32_t)(K >> (a.ushift + 5)) * 2;
+
+  const int c = wave * CW + lane;
+  const bool act = lane < CW && c < C;
+  const int ci = act ? c : 0;
+  const uint32_t voff = (uint32_t)ci * (4 * NW);
+  uint32_t vsb[UPL];
+#pragma unroll
+  for (int t = 0; t < UPL; ++t) vsb[t] = (uint32_t)((ci * UPL + t) >> a.ushift) * 2;
+
+  // Buffer views of an item's rows of each projection (rows past N read zero).
+  auto views = [&](int4 tl, int64_t row0, bool live, Rsrc (&rc)[NB], Rsrc (&rs)[NB],
+                   Rsrc (&rb)[NB]) {
+    const int64_t left = N - row0;
+    const uint32_t rows = live ? (uint32_t)(left < ROWS ? left : ROWS) : 0u;
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const QmmProblem& pb = a.p[q];
+      const int64_t e = tl.x;
+      rc[q] = make_rsrc((const char*)(pb.codes + e * pb.expert_stride_codes) + row0 * rowbytes,
+                        rows * rowbytes);
+      const int64_t sb0 = e * pb.expert_stride_sb * 2 + row0 * sbrow;
+      rs[q] = make_rsrc((const char*)pb.scales + sb0, rows * sbrow);
+      rb[q] = make_rsrc((const char*)pb.biases + sb0, rows * sbrow);
+    }
+  };
+  // Ring slot r holds row r / NB of projection r % NB.
+  auto load_row = [&](const Rsrc (&rc)[NB], const Rsrc (&rs)[NB], const Rsrc (&rb)[NB], int r,
+                      RowSlot<NW, UPL>& slot) {
+    const int q = r % NB, rr = r / NB;
+    load_chunk<NW>(rc[q], voff + rr * rowbytes, slot.w);
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) {
+      slot.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs[q], vsb[t] + rr * sbrow, 0, 0);
+      slot.b[t] = __builtin_amdgcn_raw_buffer_load_b16(rb[q], vsb[t] + rr * sbrow, 0, 0);
+    }
+  };
+  XState xs[UPL][MT];
+  auto load_x = [&](const TileRows<MT>& tr) {
+    jqd::XRaw xr[UPL][MT];
+#pragma unroll
+    for (int t = 0; t < UPL; ++t)
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        jqd::load_xraw((const uint16_t*)a.p[0].x + tr.xrow[m] * K + (int64_t)(ci * UPL + t) * 32,
+                       xr[t][m]);
+#pragma unroll
+    for (int t = 0; t < UPL; ++t)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        jqd::XRaw& r = xr[t][m];
+        const bool live = act && tr.xlive[m];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) r.d[i] = live ? r.d[i] : 0u;
+        make_xstate<D>(r, xs[t][m]);
+      }
+  };
+
+  int it = first;
+  int tile = it / a.nrb;
+  int rbi = it - tile * a.nrb;
+  int4 tl = a.plan.tiles[tile];
+  TileRows<MT> tr;
+  tile_rows<MT>(a.plan, tl, tr);
+  int64_t row0 = (int64_t)rbi * ROWS;
+  Rsrc rc[NB], rs[NB], rbv[NB];
+  views(tl, row0, true, rc, rs, rbv);
+  RowSlot<NW, UPL> ring[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    load_row(rc, rs, rbv, r, ring[r]);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  load_x(tr);
+  const Bases<D> bs = jqd::make_bases<D>();
+
+  for (int par = 0;; par ^= 1) {
+    const bool more = it + 1 < end;
+    const bool wrap = rbi + 1 == a.nrb;
+    const int tile2 = more && wrap ? tile + 1 : tile;
+    const int rbi2 = more ? (wrap ? 0 : rbi + 1) : rbi;
+    const int4 tl2 = a.plan.tiles[tile2];
+    const int64_t row02 = (int64_t)rbi2 * ROWS;
+    Rsrc rc2[NB], rs2[NB], rb2[NB];
+    views(tl2, row02, more, rc2, rs2, rb2);
+
+    float acc[RB][MT];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
+#pragma unroll
+      for (int t = 0; t < UPL; ++t) {
+        const float sv = sb_to_f32<SB>(ring[r].s[t]);
+        const float bv = sb_to_f32<SB>(ring[r].b[t]);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const float d = unit_dot<D>(ring[r].w + t * BITS, bs, xs[t][m]);
+          acc[r][m] = fmaf(sv, d + xs[t][m].O, fmaf(bv, xs[t][m].X, acc[r][m]));
+        }
+      }
+      // Row r is consumed before its slot is reloaded (see the dense GEMV).
+#pragma unroll
+      for (int m = 0; m < MT; ++m) asm volatile("" : "+v"(acc[r][m])::"memory");
+      load_row(rc2, rs2, rb2, r, ring[r]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float v = wave_total_lane63(acc[r][m]);
+        if (lane == 63) red[par][wave][r * MT + m] = v;
+      }
+    __syncthreads();
+    if (wave == 0 && lane < ROWS * MT) {
+      const int j = lane / MT, m = lane % MT;
+      int64_t orow = tr.orow[0];
+      bool live = 0 < tr.nrows;
+#pragma unroll
+      for (int q = 1; q < MT; ++q)
+        if (m == q) orow = tr.orow[q], live = q < tr.nrows;
+      const int64_t row = row0 + j;
+      if (live && row < N) {
+        float v = 0.f;
+        for (int w = 0; w < KW; ++w) v += red[par][w][(NB * j) * MT + m];
+        if constexpr (NB == 2) {
+          float u = 0.f;
+          for (int w = 0; w < KW; ++w) u += red[par][w][(NB * j + 1) * MT + m];
+          const float g = round_out(v, a.yd), up = round_out(u, a.yd);
+          v = g / (1.0f + expf(-g)) * up;
+        }
+        store_out(a.p[0].y, orow * N + row, v, a.yd);
+      }
+    }
+    if (!more) break;
+    if (tile2 != tile) {
+      // New tile: its activation rows replace the registers (the ring keeps the next rows).
+      tile_rows<MT>(a.plan, tl2, tr);
+      load_x(tr);
+    }
+    it += 1;
+    tile = tile2;
+    rbi = rbi2;
+    tl = tl2;
+    row0 = row02;
+#pragma unroll
+    for (int q = 0; q < NB; ++q) rc[q] = rc2[q], rs[q] = rs2[q], rbv[q] = rb2[q];
+  }
+}
+
+template <class D, int SB, int MT, int RB, int NB>
+int launch_g(GatherArgs& a, int64_t max_tiles, hipStream_t st) {
+  int kws = 0;
+  const int kw = gemv_waves(a.p[0].K, D::BITS, &kws);
+  if (kw > kMaxWaves) return JQ_ERR_SHAPE;
+  a.kwshift = kws;
+  constexpr int ROWS = RB / NB;
+  const int64_t nrb = (a.p[0].N + ROWS - 1) / ROWS;
+  const int64_t max_items = max_tiles * nrb;
+  if (nrb == 0 || max_items == 0) return JQ_OK;
+  if (max_items >= ((int64_t)1 << 31)) return JQ_ERR_SHAPE;
+  a.nrb = (int)nrb;
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_gather_kernel<D, SB, MT, RB, NB>,
+                                                   64 * kw, 0) != hipSuccess || nb < 1)
+    nb = 1;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  const int64_t cap = (int64_t)nb * cus;
+  const int grid = (int)(max_items < cap ? max_items : cap);
+  gemv_gather_kernel<D, SB, MT, RB, NB><<<grid, 64 * kw, 0, st>>>(a);
+  return jqh::launch_status();
+}
+
+// Rows in flight per lane: 4 rows of one projection, or 4 rows each of gate and up.
+template <class D, int SB, int NB>
+int launch_mt(GatherArgs& a, int mt, int64_t max_tiles, hipStream_t st) {
+  constexpr int RB = 4 * NB;
+  if (mt == 1) return launch_g<D, SB, 1, RB, NB>(a, max_tiles, st);
+  if (mt == 2) return launch_g<D, SB, 2, RB, NB>(a, max_tiles, st);
+  if constexpr (D::BITS != 2) {
+    if (mt == 4) return launch_g<D, SB, 4, RB, NB>(a, max_tiles, st);
+  }
+  return JQ_ERR_SHAPE;
+}
+
+template <int BITS, int XDT, int NB>
+int launch_sb(GatherArgs& a, int sb, int mt, int64_t max_tiles, hipStream_t st) {
+  using D = Dc<BITS, 64, XDT>;  // the group size is a run-time argument of this kernel
+  if (sb == JQ_BF16) return launch_mt<D, JQ_BF16, NB>(a, mt, max_tiles, st);
+  return launch_mt<D, JQ_F16, NB>(a, mt, max_tiles, st);
+}
+
+template <int BITS, int NB>
+int launch_x(GatherArgs& a, int xd, int sb, int mt, int64_t max_tiles, hipStream_t st) {
+  if (xd == JQ_BF16) return launch_sb<BITS, JQ_BF16, NB>(a, sb, mt, max_tiles, st);
+  return launch_sb<BITS, JQ_F16, NB>(a, sb, mt, max_tiles, st);
+}
+
+template <int NB>
+int launch_bits(GatherArgs& a, int bits, int xd, int sb, int mt, int64_t max_tiles,
+                hipStream_t st) {
+  switch (bits) {
+    case 2: return launch_x<2, NB>(a, xd, sb, mt, max_tiles, st);
+    case 3: return launch_x<3, NB>(a, xd, sb, mt, max_tiles, st);
+    case 4: return launch_x<4, NB>(a, xd, sb, mt, max_tiles, st);
+    case 5: return launch_x<5, NB>(a, xd, sb, mt, max_tiles, st);
+    case 6: return launch_x<6, NB>(a, xd, sb, mt, max_tiles, st);
+    default: return launch_x<8, NB>(a, xd, sb, mt, max_tiles, st);
+  }
+}
+
+}  // namespace
+
+namespace jqk {
+
+int gemv_gather_max_rows(int bits) { return bits == 2 ? 2 : 4; }
+
+bool gemv_gather_ok(int64_t N, int64_t K, int bits, int gs, int xd, int sb) {
+  if (xd != JQ_BF16 && xd != JQ_F16) return false;
+  if (sb != JQ_BF16 && sb != JQ_F16) return false;
+  if (gs != 32 && gs != 64 && gs != 128) return false;
+  const int64_t chunk = bits == 2 ? 64 : 32;  // K of one lane chunk
+  if (K <= 0 || K % chunk || gemv_waves(K, bits, nullptr) > kMaxWaves) return false;
+  // Byte offsets inside an item's buffer views stay far below 2^31.
+  return (N + 64) * (K / gs) * 2 < ((int64_t)1 << 31) && K * bits / 8 < ((int64_t)1 << 24);
+}
+
+int gemv_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPlan& plan,
+                       int64_t max_tiles, int tile_rows, int bits, int gs, int xd, int sb,
+                       int yd, hipStream_t st) {
+  if (max_tiles == 0 || p.N == 0) return JQ_OK;
+  if (!gemv_gather_ok(p.N, p.K, bits, gs, xd, sb) || tile_rows < 1 ||
+      tile_rows > gemv_gather_max_rows(bits) || (tile_rows & (tile_rows - 1)))
+    return JQ_ERR_SHAPE;
+  GatherArgs a;
+  a.p[0] = p;
+  a.p[1] = p2 ? *p2 : p;
+  a.plan = plan;
+  a.ushift = gs == 32 ? 0 : gs == 64 ? 1 : 2;
+  a.yd = yd;
+  if (p2) return launch_bits<2>(a, bits, xd, sb, tile_rows, max_tiles, st);
+  return launch_bits<1>(a, bits, xd, sb, tile_rows, max_tiles, st);
+}
+
+}  // namespace jqk

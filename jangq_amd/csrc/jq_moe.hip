@@ -16,9 +16,11 @@ namespace {
 using namespace jq;
 
 // Rows per tile of the grouped kernels: 16 for the LDS-staged GEMM, 16/8/4 (gs 128/64/32)
-// for the decode kernel. Workspaces are sized for the smallest tile.
+// for the matrix-core decode kernel, 1/2/4 for the vector-ALU gather GEMV, which only runs
+// up to kGemvRows plan rows. Workspaces are sized for the smallest tile they may get.
 constexpr int kMinTileRows = 4;
 constexpr int kGemmTileRows = 16;
+constexpr int64_t kGemvRows = 4096;
 constexpr int kMaxExperts = 4096;
 
 // One wave per token. Lanes hold E/64 logits each; top-k by k rounds of wave argmax
@@ -103,8 +105,8 @@ JQ_DEV int block_exclusive_scan(int v, int* sh_wave, int& total) {
 //   seg_off[E+1]  exclusive offsets of each expert's segment in `order`
 //   order         pair ids grouped by expert (order inside a segment is arbitrary: it does
 //                 not change any value). Pairs whose expert id is >= E are left out.
-//   tiles         (expert, first row, rows) for every tile_rows-row tile of every segment
-//                 (segment rows = count * M)
+//   tiles         (expert, first row, rows, segment offset) for every tile_rows-row tile of
+//                 every segment (segment rows = count * M)
 //   n_tiles[0]    number of tiles
 __global__ void __launch_bounds__(1024) plan_kernel(const uint32_t* __restrict__ rhs, int n_pairs,
                                                     int E, int M, int tile_rows, int* seg_off,
@@ -137,7 +139,7 @@ __global__ void __launch_bounds__(1024) plan_kernel(const uint32_t* __restrict__
     cur[e] = base;
     const int rows = cnt[e] * M;
     for (int r = 0; r < rows; r += tile_rows) {
-      tiles[tbase++] = make_int4(e, r, rows - r < tile_rows ? rows - r : tile_rows, 0);
+      tiles[tbase++] = make_int4(e, r, rows - r < tile_rows ? rows - r : tile_rows, base);
     }
     base += cnt[e];
   }
@@ -168,7 +170,8 @@ inline WsLayout ws_layout(int64_t n_pairs, int64_t E, int64_t M) {
   int64_t o = 0;
   L.seg_off = o; o = align256(o + (E + 1) * 4);
   L.order = o; o = align256(o + n_pairs * 4);
-  L.tiles = o; o = align256(o + max_tiles_for(n_pairs, E, M, kMinTileRows) * 16);
+  const int min_tile = n_pairs * M <= kGemvRows ? 1 : kMinTileRows;
+  L.tiles = o; o = align256(o + max_tiles_for(n_pairs, E, M, min_tile) * 16);
   L.n_tiles = o; o = align256(o + 4);
   L.total = o;
   return L;
@@ -193,12 +196,49 @@ int build_plan(const uint32_t* rhs, int64_t n_pairs, int64_t E, int64_t M, int t
   return jqh::launch_status();
 }
 
-// Decode-sized grouped problems (few rows per selected expert) run on the streaming decode
-// kernel; larger ones on the LDS-staged GEMM with 16-row tiles.
-bool use_decode_kernel(int64_t rows, int64_t E, int64_t n_pairs, int gs, int xd, int sb) {
-  if (!((xd == JQ_BF16 || xd == JQ_F16) && (sb == JQ_BF16 || sb == JQ_F16))) return false;
+// Kernel for a grouped problem of `rows` plan rows over the active experts.
+//   gemv: few rows per active expert (decode); tiles of 1, 2 or 4 rows, as many as the average
+//         rows per active expert, up to what the kernel holds in registers.
+//   dec:  up to two decode tiles per active expert on average (matrix cores, streaming).
+//   gemm: larger problems, LDS-staged matrix-core GEMM with 16-row tiles.
+enum class Kern { gemv, dec, gemm };
+
+struct Choice {
+  Kern k;
+  int tile_rows;
+};
+
+// One projection per entry of bits/N/K (gate|up and down share a plan in SwitchGLU).
+Choice choose(int64_t rows, int64_t E, int64_t n_pairs, int gs, int xd, int sb, int nproj,
+              const int* bits, const int64_t* N, const int64_t* K) {
+  const bool dt = (xd == JQ_BF16 || xd == JQ_F16) && (sb == JQ_BF16 || sb == JQ_F16);
   const int64_t active = n_pairs < E ? n_pairs : E;
-  return rows <= 2 * active * jqk::dec_tokens_per_block(gs);
+  const int64_t avg = (rows + active - 1) / (active > 0 ? active : 1);
+  if (dt && rows <= kGemvRows) {
+    bool ok = true;
+    int maxr = 4;
+    for (int i = 0; i < nproj; ++i) {
+      ok = ok && jqk::gemv_gather_ok(N[i], K[i], bits[i], gs, xd, sb);
+      const int m = jqk::gemv_gather_max_rows(bits[i]);
+      maxr = m < maxr ? m : maxr;
+    }
+    if (ok && avg <= 2 * maxr) {
+      const int tr = avg <= 1 ? 1 : avg <= 2 ? 2 : 4;
+      return {Kern::gemv, tr < maxr ? tr : maxr};
+    }
+  }
+  if (dt && rows <= 2 * active * jqk::dec_tokens_per_block(gs))
+    return {Kern::dec, jqk::dec_tokens_per_block(gs)};
+  return {Kern::gemm, kGemmTileRows};
+}
+
+int grouped_launch(const Choice& c, const jqk::QmmProblem& p, const jqk::QmmProblem* p2,
+                   const jqk::GatherPlan& plan, int64_t mt, int bits, int gs, int xd, int sb,
+                   int yd, hipStream_t st) {
+  if (c.k == Kern::gemv)
+    return jqk::gemv_gather_launch(p, p2, plan, mt, c.tile_rows, bits, gs, xd, sb, yd, st);
+  if (c.k == Kern::dec) return jqk::dec_gather_launch(p, p2, plan, mt, bits, gs, xd, sb, yd, st);
+  return jqk::qmm_gather_launch(p, p2, plan, mt, bits, gs, xd, sb, yd, st);
 }
 
 int check_expert_shape(int bits, int gs, int64_t E, int64_t N, int64_t K) {
@@ -246,9 +286,9 @@ int jq_gather_qmm(const void* x, int x_dtype, int64_t x_batch, int64_t M, const 
   hipStream_t st = (hipStream_t)stream;
   jqk::GatherPlan plan;
   (void)sorted_indices;  // grouping is done on the device in every case
-  const bool dec = use_decode_kernel(n_pairs * M, E, n_pairs, group_size, x_dtype, sb_dtype);
-  const int tile_rows = dec ? jqk::dec_tokens_per_block(group_size) : kGemmTileRows;
-  s = build_plan(rhs, n_pairs, E, M, tile_rows, workspace, plan, lhs, st);
+  const int64_t Nv[1] = {N}, Kv[1] = {K};
+  const Choice c = choose(n_pairs * M, E, n_pairs, group_size, x_dtype, sb_dtype, 1, &bits, Nv, Kv);
+  s = build_plan(rhs, n_pairs, E, M, c.tile_rows, workspace, plan, lhs, st);
   if (s) return s;
   plan.x_rows = x_batch * M;
   jqk::QmmProblem p;
@@ -262,11 +302,8 @@ int jq_gather_qmm(const void* x, int x_dtype, int64_t x_batch, int64_t M, const 
   p.K = K;
   p.expert_stride_codes = N * (K * bits / 32);
   p.expert_stride_sb = N * (K / group_size);
-  const int64_t mt = max_tiles_for(n_pairs, E, M, tile_rows);
-  if (dec) return jqk::dec_gather_launch(p, nullptr, plan, mt, bits, group_size, x_dtype, sb_dtype,
-                                         y_dtype, st);
-  return jqk::qmm_gather_launch(p, nullptr, plan, mt, bits, group_size, x_dtype, sb_dtype,
-                                y_dtype, st);
+  const int64_t mt = max_tiles_for(n_pairs, E, M, c.tile_rows);
+  return grouped_launch(c, p, nullptr, plan, mt, bits, group_size, x_dtype, sb_dtype, y_dtype, st);
 }
 
 int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E,
@@ -294,10 +331,11 @@ int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, i
   hipStream_t st = (hipStream_t)stream;
   // Pair i = t*k + j uses x row t = i / k and expert idx[i]; one plan serves both launches
   // (gate+up reads x rows i / k, down reads h rows i).
-  const bool dec = use_decode_kernel(n_pairs, E, n_pairs, group_size, x_dtype, sb_dtype);
-  const int tile_rows = dec ? jqk::dec_tokens_per_block(group_size) : kGemmTileRows;
+  const int bv[2] = {bits_gu, bits_d};
+  const int64_t Nv[2] = {I, H}, Kv[2] = {H, I};
+  const Choice c = choose(n_pairs, E, n_pairs, group_size, x_dtype, sb_dtype, 2, bv, Nv, Kv);
   jqk::GatherPlan plan;
-  s = build_plan(idx, n_pairs, E, 1, tile_rows, workspace, plan, nullptr, st);
+  s = build_plan(idx, n_pairs, E, 1, c.tile_rows, workspace, plan, nullptr, st);
   if (s) return s;
   jqk::GatherPlan plan_gu = plan;
   plan_gu.lhs = nullptr;
@@ -311,20 +349,15 @@ int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, i
   g.expert_stride_sb = I * (H / group_size);
   u = g;
   u.codes = up_codes; u.scales = up_scales; u.biases = up_biases;
-  const int64_t mt = max_tiles_for(n_pairs, E, 1, tile_rows);
-  s = dec ? jqk::dec_gather_launch(g, &u, plan_gu, mt, bits_gu, group_size, x_dtype, sb_dtype,
-                                   y_dtype, st)
-          : jqk::qmm_gather_launch(g, &u, plan_gu, mt, bits_gu, group_size, x_dtype, sb_dtype,
-                                   y_dtype, st);
+  const int64_t mt = max_tiles_for(n_pairs, E, 1, c.tile_rows);
+  s = grouped_launch(c, g, &u, plan_gu, mt, bits_gu, group_size, x_dtype, sb_dtype, y_dtype, st);
   if (s) return s;
   d.x = h_buf; d.codes = down_codes; d.scales = down_scales; d.biases = down_biases; d.y = out;
   d.M = 1; d.N = H; d.K = I;
   d.expert_stride_codes = H * (I * bits_d / 32);
   d.expert_stride_sb = H * (I / group_size);
-  if (dec) return jqk::dec_gather_launch(d, nullptr, plan, mt, bits_d, group_size, y_dtype,
-                                         sb_dtype, y_dtype, st);
-  return jqk::qmm_gather_launch(d, nullptr, plan, mt, bits_d, group_size, y_dtype, sb_dtype,
-                                y_dtype, st);
+  return grouped_launch(c, d, nullptr, plan, mt, bits_d, group_size, y_dtype, sb_dtype, y_dtype,
+                        st);
 }
 
 }  // extern "C"

@@ -44,7 +44,7 @@ bool gemm_ok(int64_t M, int64_t K, int bits, int gs, int xd, int sb);
 struct GatherPlan {
   const uint32_t* order;     // [n_pairs] pair ids grouped by expert
   const int* seg_off;        // [E + 1] segment offsets into order
-  const int4* tiles;         // [max_tiles] (expert, first row, rows, 0)
+  const int4* tiles;         // [max_tiles] (expert, first row, rows, seg_off[expert])
   const int* n_tiles;        // [1] number of valid tiles
   const uint32_t* lhs;       // [n_pairs] or NULL
   int M;                     // rows per pair
@@ -83,5 +83,13 @@ int dec_dense_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int
 int dec_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPlan& plan,
                       int64_t max_tiles, int bits, int gs, int xd, int sb, int yd,
                       hipStream_t st);
+
+// Expert-gathered decode GEMV on the vector ALUs (jq_gemv_gather.hip): plan tiles of
+// tile_rows (1, 2 or 4, at most gemv_gather_max_rows) rows; p2 as for qmm_gather_launch.
+int gemv_gather_max_rows(int bits);
+bool gemv_gather_ok(int64_t N, int64_t K, int bits, int gs, int xd, int sb);
+int gemv_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPlan& plan,
+                       int64_t max_tiles, int tile_rows, int bits, int gs, int xd, int sb,
+                       int yd, hipStream_t st);
 
 }  // namespace jqk
