@@ -34,6 +34,7 @@ EXTRA = {
     "jq_codec.hip": ["-ffp-contract=off"],
     # decode kernels: keep MFMA results in VGPRs (no accumulator-register round trips)
     "jq_dec.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "jq_decp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

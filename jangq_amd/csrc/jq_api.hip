@@ -9,6 +9,9 @@ namespace {
 // Activation rows from which the 256 x 256-tile prefill GEMM takes over (measured on MI355X
 // at K = 4096, N = 14336: faster than the 128-row-tile GEMM from 384 rows on).
 constexpr int64_t kGemmMinRows = 384;
+// Activation rows up to which the persistent decode-batch kernel runs (in passes of
+// 2 * 16/(128/gs) rows, the weights re-read from the last-level cache after the first).
+constexpr int64_t kDecpMaxRows = 64;
 
 int dense_one(const void* x, int xd, const uint32_t* codes, const void* scales,
               const void* biases, int sb, int bits, int gs, int64_t M, int64_t N, int64_t K,
@@ -23,13 +26,13 @@ int dense_one(const void* x, int xd, const uint32_t* codes, const void* scales,
     b.p[0].y = y; b.p[0].N = N;
     return jqk::gemv_launch(b, 1, bits, gs, xd, sb, yd, st);
   }
-  if (jqk::dec_dense_ok((int)(M < (1 << 30) ? M : (1 << 30)), K, gs, xd, sb)) {
+  if (M <= kDecpMaxRows && jqk::decp_ok(Mi, K, N, xd, sb)) {
     jqk::QmvBatch b;
-    b.M = (int)M;
+    b.M = Mi;
     b.K = (int)K;
     b.p[0].x = x; b.p[0].codes = codes; b.p[0].scales = scales; b.p[0].biases = biases;
     b.p[0].y = y; b.p[0].N = N;
-    return jqk::dec_dense_launch(b, 1, bits, gs, xd, sb, yd, st);
+    return jqk::decp_launch(b, 1, bits, gs, xd, sb, yd, st);
   }
   if (M >= kGemmMinRows && jqk::gemm_ok(M, K, bits, gs, xd, sb)) {
     jqk::QmmProblem p;
@@ -129,7 +132,7 @@ int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
   int64_t maxN = 0;
   for (int i = 0; i < count; ++i) maxN = N[i] > maxN ? N[i] : maxN;
   const bool gemv = same && jqk::gemv_ok(M0, K[0], maxN, bits[0], group_size[0], x_dtype, sb_dtype);
-  const bool dec = same && jqk::dec_dense_ok(M0, K[0], group_size[0], x_dtype, sb_dtype);
+  const bool dec = same && M[0] <= kDecpMaxRows && jqk::decp_ok(M0, K[0], maxN, x_dtype, sb_dtype);
   if (gemv || dec || (same && M[0] >= 1 && M[0] <= 4 && K[0] > 0)) {
     jqk::QmvBatch b;
     b.M = (int)M[0];
@@ -146,7 +149,7 @@ int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
       ++n;
     }
     if (gemv) return jqk::gemv_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
-    if (dec) return jqk::dec_dense_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
+    if (dec) return jqk::decp_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
     return jqk::qmv_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
   }
   for (int i = 0; i < count; ++i) {

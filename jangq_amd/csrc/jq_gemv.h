@@ -116,6 +116,9 @@ JQ_DEV void load_chunk(Rsrc r, uint32_t voff, uint32_t* w) {
     const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
     w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
     w[4] = u[0]; w[5] = u[1]; w[6] = u[2]; w[7] = u[3];
+  } else if constexpr (NW == 2) {
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    w[0] = v[0]; w[1] = v[1];
   } else if constexpr (NW == 3) {
     const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, 0);
     w[0] = v[0]; w[1] = v[1]; w[2] = v[2];

@@ -84,6 +84,12 @@ int dec_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPla
                       int64_t max_tiles, int bits, int gs, int xd, int sb, int yd,
                       hipStream_t st);
 
+// Persistent decode-batch matrix-core kernel (jq_decp.hip): any M (passes of up to
+// 2 * 16/(128/gs) activation rows), K % 128 == 0, bf16/f16 activations and scales.
+bool decp_ok(int M, int64_t K, int64_t maxN, int xd, int sb);
+int decp_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
+                hipStream_t st);
+
 // Expert-gathered decode GEMV on the vector ALUs (jq_gemv_gather.hip): plan tiles of
 // tile_rows (1, 2 or 4, at most gemv_gather_max_rows) rows; p2 as for qmm_gather_launch.
 int gemv_gather_max_rows(int bits);
