@@ -35,6 +35,7 @@ EXTRA = {
     # decode kernels: keep MFMA results in VGPRs (no accumulator-register round trips)
     "jq_dec.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "jq_decp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "jq_qmv4.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -84,6 +84,12 @@ int dec_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPla
                       int64_t max_tiles, int bits, int gs, int xd, int sb, int yd,
                       hipStream_t st);
 
+// Decode GEMV on 4x4x4 matrix-core blocks (jq_qmv4.hip): passes of up to 8 activation rows,
+// K % 32 == 0, bf16/f16 activations and scales.
+bool qmv4_ok(int M, int64_t K, int64_t maxN, int bits, int gs, int xd, int sb);
+int qmv4_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
+                hipStream_t st);
+
 // Persistent decode-batch matrix-core kernel (jq_decp.hip): any M (passes of up to
 // 2 * 16/(128/gs) activation rows), K % 128 == 0, bf16/f16 activations and scales.
 bool decp_ok(int M, int64_t K, int64_t maxN, int xd, int sb);

@@ -112,6 +112,22 @@ def test_c2_projection_shapes(N, K, bits):
     run_case(8, N, K, bits, 64, seed=N + bits + 1)
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_long_row_decode_batches(bits, gs):
+    """Decode batches of long rows (K >= 8192: the 4x4x4 matrix-core GEMV, passes of 4 or 8
+    rows; wider codes at K = 12288 fall to the persistent kernel), ragged N, bf16 and f16."""
+    for M, N, K in ((5, 44, 8192), (8, 37, 8192), (13, 21, 12288)):
+        run_case(M, N, K, bits, gs, seed=M * 7 + bits + gs)
+    run_case(6, 30, 8192, bits, gs, xdt="f16", sidecar="f16", seed=bits + gs)
+
+
+@pytest.mark.parametrize("M", [5, 8, 32])
+def test_c2_down_projection_batches(M):
+    """Config 2 down projection (4096 x 14336, 2-bit) at decode batches 5, 8 and 32."""
+    run_case(M, 4096, 14336, 2, 64, seed=900 + M)
+
+
 def test_multi_matches_single():
     K = 1024
     ws = [QWeight(n, K, 6, 64, seed=i) for i, n in enumerate((256, 64, 64))]
