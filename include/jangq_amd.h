@@ -177,6 +177,35 @@ int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, i
                   int bits_d, int sb_dtype, int group_size, void* h_buf, void* out,
                   int y_dtype, void* workspace, int64_t workspace_bytes, jq_stream_t stream);
 
+/*
+ * Weighted combine of the routed experts' outputs (and the shared expert's):
+ *   out[t, :] = round(sum_j w[t, j] * y[t, j, :])        fp32 in slot order j = 0 .. k-1
+ *   out[t, :] = round(out[t, :] + shared[t, :])           if shared != NULL
+ * y [T, k, H], shared [T, H] and out [T, H] of `dtype` (JQ_BF16 / JQ_F16 / JQ_F32); w f32 [T, k].
+ * No MLX operator: one launch for the caller-side composition (y * scores[..., None]).sum(-2)
+ * (+ shared_expert(x)) of jang-tools/jang_tools/qwen4_exp/modeling.py:594-597, with the same
+ * two roundings as those array operations.
+ */
+int jq_moe_combine(const void* y, const float* w, const void* shared, int64_t T, int k,
+                   int64_t H, void* out, int dtype, jq_stream_t stream);
+
+/*
+ * SwiGLU projection pair of a dense MLP: h = silu(round(x @ Wg^T)) * round(x @ Wu^T), each
+ * product rounded to y_dtype first (as two quantized_matmul calls returning y_dtype give),
+ * h rounded to y_dtype. Gate and up share bits, group size, N and K.
+ * up_buf: caller scratch of M*N elements of y_dtype, used when M is above the decode sizes
+ * (M > 4; 2-bit: M > 2); NULL is accepted for decode sizes (one launch, no scratch).
+ * No MLX operator as one call: replaces gate_proj(x), up_proj(x) and silu(g) * u of the
+ * shared-expert MLP (jang-tools/jang_tools/qwen4_exp/modeling.py:597,
+ * jang-tools/jang_tools/dsv41/metal_decode.py:355-371 for the shared slot).
+ */
+int jq_quantized_swiglu(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
+                        const uint32_t* gate_codes, const void* gate_scales,
+                        const void* gate_biases, const uint32_t* up_codes,
+                        const void* up_scales, const void* up_biases, int sb_dtype, int bits,
+                        int group_size, void* h, void* up_buf, int y_dtype,
+                        jq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,6 +33,11 @@ SIGNATURES = {
         _I,
         [_P, _I, _L, _L, _P, _P, _P, _I, _I, _I, _L, _L, _L, _P, _P, _L, _I, _P, _I, _P, _L, _P],
     ),
+    "jq_moe_combine": (_I, [_P, _P, _P, _L, _I, _L, _P, _I, _P]),
+    "jq_quantized_swiglu": (
+        _I,
+        [_P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P],
+    ),
     "jq_switch_glu": (
         _I,
         [_P, _I, _L, _L, _L, _L, _P, _I,

@@ -66,12 +66,23 @@ JQ_DEV void tile_rows(const GatherPlan& pl, int4 tl, TileRows<MT>& tr) {
     const int rr = tl.y + (m < tl.z ? m : 0);
     const int Mp = pl.M;
     const int pi = Mp == 1 ? rr : rr / Mp, mi = Mp == 1 ? 0 : rr - pi * Mp;
-    const uint32_t pair = pl.order[tl.w + pi];
+    const uint32_t pair = pl.order ? pl.order[tl.w + pi] : (uint32_t)(tl.w + pi);
     const int64_t xr = (int64_t)(pl.lhs ? pl.lhs[pair] : pair / (uint32_t)pl.pair_div) * Mp + mi;
     tr.xlive[m] = m < tl.z && xr < pl.x_rows;
     tr.xrow[m] = tr.xlive[m] ? xr : 0;
     tr.orow[m] = (int64_t)pair * Mp + mi;
   }
+}
+
+// Tile t of the plan, or in direct mode pairs [t*R, t*R + R) of expert rhs[t*R] (0 rows if
+// the id is out of range).
+JQ_DEV int4 get_tile(const GatherPlan& pl, int t) {
+  if (pl.tiles) return pl.tiles[t];
+  const int r0 = t * pl.direct_rows;
+  const int left = pl.direct_pairs - r0;
+  const uint32_t e = pl.rhs ? pl.rhs[r0] : 0u;
+  const bool ok = e < (uint32_t)pl.E;
+  return make_int4(ok ? (int)e : 0, 0, ok ? (left < pl.direct_rows ? left : pl.direct_rows) : 0, r0);
 }
 
 template <class D, int SB, int MT, int RB, int NB>
@@ -82,7 +93,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
   constexpr int ROWS = RB / NB;  // weight rows of one projection per item
   __shared__ float red[2][kMaxWaves][RB * MT];
 
-  const int items = *a.plan.n_tiles * a.nrb;
+  const int ntiles = a.plan.n_tiles ? *a.plan.n_tiles
+                                     : (a.plan.direct_pairs + a.plan.direct_rows - 1) / a.plan.direct_rows;
+  const int items = ntiles * a.nrb;
   const int per = (items + (int)gridDim.x - 1) / (int)gridDim.x;
   const int first = blockIdx.x * per;
   const int end = first + per < items ? first + per : items;
@@ -109,7 +122,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
   auto views = [&](int4 tl, int64_t row0, bool live, Rsrc (&rc)[NB], Rsrc (&rs)[NB],
                    Rsrc (&rb)[NB]) {
     const int64_t left = N - row0;
-    const uint32_t rows = live ? (uint32_t)(left < ROWS ? left : ROWS) : 0u;
+    const uint32_t rows = live && tl.z > 0 ? (uint32_t)(left < ROWS ? left : ROWS) : 0u;
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
       const QmmProblem& pb = a.p[q];
@@ -156,7 +169,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
   int it = first;
   int tile = it / a.nrb;
   int rbi = it - tile * a.nrb;
-  int4 tl = a.plan.tiles[tile];
+  int4 tl = get_tile(a.plan, tile);
   TileRows<MT> tr;
   tile_rows<MT>(a.plan, tl, tr);
   int64_t row0 = (int64_t)rbi * ROWS;
@@ -177,7 +190,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
     const bool wrap = rbi + 1 == a.nrb;
     const int tile2 = more && wrap ? tile + 1 : tile;
     const int rbi2 = more ? (wrap ? 0 : rbi + 1) : rbi;
-    const int4 tl2 = a.plan.tiles[tile2];
+    const int4 tl2 = get_tile(a.plan, tile2);
     const int64_t row02 = (int64_t)rbi2 * ROWS;
     Rsrc rc2[NB], rs2[NB], rb2[NB];
     views(tl2, row02, more, rc2, rs2, rb2);

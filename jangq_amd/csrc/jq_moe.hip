@@ -23,8 +23,10 @@ constexpr int kGemmTileRows = 16;
 constexpr int64_t kGemvRows = 4096;
 constexpr int kMaxExperts = 4096;
 
-// One wave per token. Lanes hold E/64 logits each; top-k by k rounds of wave argmax
-// (ties -> lowest expert id), probabilities from a max-subtracted fp32 softmax.
+// One wave per token. Lane l holds logits l, l + 64, ... (SL = ceil(E/64) of them) in
+// registers; top-k by k rounds of wave argmax (ties -> lowest expert id), probabilities from a
+// max-subtracted fp32 softmax.
+template <int SL>
 __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ logits, int T, int E,
                                                     int k, int renorm, uint32_t* __restrict__ idx,
                                                     float* __restrict__ wout) {
@@ -32,28 +34,38 @@ __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ lo
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const float* row = logits + (int64_t)t * E;
+  float v[SL];
+#pragma unroll
+  for (int i = 0; i < SL; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? row[e] : -INFINITY;
+  }
   float mx = -INFINITY;
-  for (int e = lane; e < E; e += 64) mx = fmaxf(mx, row[e]);
+#pragma unroll
+  for (int i = 0; i < SL; ++i) mx = fmaxf(mx, v[i]);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
   float sum = 0.f;
-  for (int e = lane; e < E; e += 64) sum += expf(row[e] - mx);
+#pragma unroll
+  for (int i = 0; i < SL; ++i) sum += lane + 64 * i < E ? expf(v[i] - mx) : 0.f;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
   const float inv = 1.0f / sum;
 
-  // Selection runs on the logits (softmax is monotone); chosen ones are masked by id.
-  uint64_t chosen = 0;  // per-lane bitmask over its slots (E <= 4096 -> <= 64 slots)
+  // Selection runs on the logits (softmax is monotone); a chosen slot is set to -inf and
+  // excluded by id (a chosen -inf logit cannot be picked twice).
+  bool taken[SL];
+#pragma unroll
+  for (int i = 0; i < SL; ++i) taken[i] = lane + 64 * i >= E;
   float wsum = 0.f, wsel = 0.f;
   int my_id = 0;
   for (int j = 0; j < k; ++j) {
     float best = -INFINITY;
     int bid = 0x7FFFFFFF;
-    int slot = 0;
-    for (int e = lane; e < E; e += 64, ++slot) {
-      if ((chosen >> slot) & 1ull) continue;
-      const float v = row[e];
-      if (v > best || (v == best && e < bid)) { best = v; bid = e; }
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+      const int e = lane + 64 * i;
+      if (!taken[i] && (v[i] > best || (v[i] == best && e < bid))) { best = v[i]; bid = e; }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -61,7 +73,9 @@ __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ lo
       const int oid = __shfl_xor(bid, o, 64);
       if (ov > best || (ov == best && oid < bid)) { best = ov; bid = oid; }
     }
-    if ((bid & 63) == lane) chosen |= 1ull << (bid >> 6);
+#pragma unroll
+    for (int i = 0; i < SL; ++i)
+      if (lane + 64 * i == bid) taken[i] = true;
     const float p = expf(best - mx) * inv;
     wsum += p;
     if (lane == j) { wsel = p; my_id = bid; }
@@ -189,11 +203,33 @@ int build_plan(const uint32_t* rhs, int64_t n_pairs, int64_t E, int64_t M, int t
   plan.M = (int)M;
   plan.pair_div = 1;
   plan.x_rows = 0;
+  plan.rhs = rhs;
+  plan.E = (int)E;
+  plan.direct_pairs = 0;
+  plan.direct_rows = 1;
   plan_kernel<<<1, 1024, 0, st>>>(rhs, (int)n_pairs, (int)E, (int)M, tile_rows,
                                   (int*)(base + L.seg_off),
                                   (uint32_t*)(base + L.order), (int4*)(base + L.tiles),
                                   (int*)(base + L.n_tiles));
   return jqh::launch_status();
+}
+
+// A plan without the plan kernel: every (one-row) pair is its own tile, read in pair order.
+jqk::GatherPlan direct_plan(const uint32_t* rhs, int64_t n_pairs, int64_t E, const uint32_t* lhs) {
+  jqk::GatherPlan plan;
+  plan.order = nullptr;
+  plan.seg_off = nullptr;
+  plan.tiles = nullptr;
+  plan.n_tiles = nullptr;
+  plan.lhs = lhs;
+  plan.M = 1;
+  plan.pair_div = 1;
+  plan.x_rows = 0;
+  plan.rhs = rhs;
+  plan.E = (int)E;
+  plan.direct_pairs = (int)n_pairs;
+  plan.direct_rows = 1;
+  return plan;
 }
 
 // Kernel for a grouped problem of `rows` plan rows over the active experts.
@@ -248,17 +284,151 @@ int check_expert_shape(int bits, int gs, int64_t E, int64_t N, int64_t K) {
   return JQ_OK;
 }
 
+// out[t, i] = round(sum_j w[t, j] * y[t, j, i]) (fp32, slot order), then round(+ shared[t, i]).
+// One thread per 8 consecutive elements of a row (H % 8 == 0) or per element.
+template <int DT, int VEC>
+__global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ y,
+                                                      const float* __restrict__ w,
+                                                      const void* __restrict__ shared, int64_t T,
+                                                      int k, int64_t H, void* __restrict__ out) {
+  const int64_t per_row = H / VEC;
+  const int64_t n = T * per_row;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / per_row, c = (i - t * per_row) * VEC;
+    float acc[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] = 0.f;
+    for (int j = 0; j < k; ++j) {
+      const float wj = w[t * k + j];
+      const int64_t base = (t * k + j) * H + c;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = fmaf(wj, load_t<DT>(y, base + v), acc[v]);
+    }
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      float r = acc[v];
+      if constexpr (DT != JQ_F32) {
+        r = DT == JQ_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(r))
+                          : f16_bits_to_f32(f32_to_f16_bits(r));
+      }
+      if (shared) r += load_t<DT>(shared, t * H + c + v);
+      store_t<DT>(out, t * H + c + v, r);
+    }
+  }
+}
+
+// h = round(silu(g) * u) elementwise (g, u already rounded to the output dtype).
+template <int DT>
+__global__ void __launch_bounds__(256) swiglu_kernel(const void* __restrict__ g,
+                                                     const void* __restrict__ u, int64_t n,
+                                                     void* __restrict__ h) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float gv = load_t<DT>(g, i), uv = load_t<DT>(u, i);
+    store_t<DT>(h, i, gv / (1.0f + expf(-gv)) * uv);
+  }
+}
+
+inline unsigned grid_for(int64_t n) {
+  const int64_t b = (n + 255) / 256;
+  return (unsigned)(b < 8192 ? (b < 1 ? 1 : b) : 8192);
+}
+
 }  // namespace
 
 extern "C" {
+
+int jq_moe_combine(const void* y, const float* w, const void* shared, int64_t T, int k,
+                   int64_t H, void* out, int dtype, jq_stream_t stream) {
+  if (T < 0 || k <= 0 || H < 0) return JQ_ERR_SHAPE;
+  if (!jqh::dtype_ok(dtype)) return JQ_ERR_DTYPE;
+  if (T == 0 || H == 0) return JQ_OK;
+  if (!y || !w || !out) return JQ_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  const bool vec = H % 8 == 0;
+  const int64_t n = T * (vec ? H / 8 : H);
+#define JQ_C(DT)                                                                             \
+  if (vec) combine_kernel<DT, 8><<<grid_for(n), 256, 0, st>>>(y, w, shared, T, k, H, out);  \
+  else combine_kernel<DT, 1><<<grid_for(n), 256, 0, st>>>(y, w, shared, T, k, H, out);
+  if (dtype == JQ_BF16) { JQ_C(JQ_BF16) }
+  else if (dtype == JQ_F16) { JQ_C(JQ_F16) }
+  else { JQ_C(JQ_F32) }
+#undef JQ_C
+  return jqh::launch_status();
+}
+
+int jq_quantized_swiglu(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
+                        const uint32_t* gate_codes, const void* gate_scales,
+                        const void* gate_biases, const uint32_t* up_codes, const void* up_scales,
+                        const void* up_biases, int sb_dtype, int bits, int group_size, void* h,
+                        void* up_buf, int y_dtype, jq_stream_t stream) {
+  int s = jqh::check_qshape(bits, group_size, N, K);
+  if (s) return s;
+  if (M < 0 || M > ((int64_t)1 << 30)) return JQ_ERR_SHAPE;
+  if (!jqh::dtype_ok(x_dtype) || !jqh::dtype_ok(sb_dtype) || !jqh::dtype_ok(y_dtype))
+    return JQ_ERR_DTYPE;
+  if (M == 0 || N == 0) return JQ_OK;
+  if (!x || !gate_codes || !gate_scales || !gate_biases || !up_codes || !up_scales ||
+      !up_biases || !h)
+    return JQ_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  // Decode sizes: one grouped launch of the expert-gathered GEMV over a single "expert" whose
+  // tile holds all M rows, with the SiLU * up epilogue.
+  const int maxr = jqk::gemv_gather_max_rows(bits);
+  if (M <= maxr && (y_dtype == JQ_BF16 || y_dtype == JQ_F16) &&
+      jqk::gemv_gather_ok(N, K, bits, group_size, x_dtype, sb_dtype)) {
+    jqk::GatherPlan plan = direct_plan(nullptr, M, 1, nullptr);
+    plan.direct_rows = (int)M;
+    plan.x_rows = M;
+    jqk::QmmProblem g, u;
+    g.x = x; g.codes = gate_codes; g.scales = gate_scales; g.biases = gate_biases; g.y = h;
+    g.M = 1; g.N = N; g.K = K;
+    g.expert_stride_codes = 0;
+    g.expert_stride_sb = 0;
+    u = g;
+    u.codes = up_codes; u.scales = up_scales; u.biases = up_biases;
+    const int tr = M <= 1 ? 1 : M <= 2 ? 2 : 4;
+    return jqk::gemv_gather_launch(g, &u, plan, 1, tr, bits, group_size, x_dtype, sb_dtype,
+                                   y_dtype, st);
+  }
+  // Otherwise: gate and up in one grouped dense launch, then the elementwise SiLU * up.
+  if (!up_buf) return JQ_ERR_WORKSPACE;
+  const void* xs[2] = {x, x};
+  const uint32_t* cs[2] = {gate_codes, up_codes};
+  const void* ss[2] = {gate_scales, up_scales};
+  const void* bs[2] = {gate_biases, up_biases};
+  const int bv[2] = {bits, bits}, gv[2] = {group_size, group_size};
+  const int64_t Mv[2] = {M, M}, Nv[2] = {N, N}, Kv[2] = {K, K};
+  void* ys[2] = {h, up_buf};
+  s = jq_quantized_matmul_multi(2, xs, x_dtype, cs, ss, bs, sb_dtype, bv, gv, Mv, Nv, Kv, ys,
+                                y_dtype, stream);
+  if (s) return s;
+  const int64_t n = M * N;
+  if (y_dtype == JQ_BF16) swiglu_kernel<JQ_BF16><<<grid_for(n), 256, 0, st>>>(h, up_buf, n, h);
+  else if (y_dtype == JQ_F16) swiglu_kernel<JQ_F16><<<grid_for(n), 256, 0, st>>>(h, up_buf, n, h);
+  else swiglu_kernel<JQ_F32><<<grid_for(n), 256, 0, st>>>(h, up_buf, n, h);
+  return jqh::launch_status();
+}
+
 
 int jq_moe_route(const float* logits, int64_t T, int64_t E, int k, int renorm, uint32_t* idx,
                  float* weights, jq_stream_t stream) {
   if (T < 0 || E <= 0 || E > kMaxExperts || k <= 0 || k > E || k > 64) return JQ_ERR_SHAPE;
   if (T == 0) return JQ_OK;
   if (!logits || !idx || !weights) return JQ_ERR_NULL;
-  route_kernel<<<(unsigned)((T + 3) / 4), 256, 0, (hipStream_t)stream>>>(
-      logits, (int)T, (int)E, k, renorm, idx, weights);
+  const unsigned grid = (unsigned)((T + 3) / 4);
+  hipStream_t st = (hipStream_t)stream;
+  const int sl = (int)((E + 63) / 64);
+#define JQ_R(SL) route_kernel<SL><<<grid, 256, 0, st>>>(logits, (int)T, (int)E, k, renorm, idx, weights)
+  if (sl <= 1) JQ_R(1);
+  else if (sl <= 2) JQ_R(2);
+  else if (sl <= 4) JQ_R(4);
+  else if (sl <= 8) JQ_R(8);
+  else if (sl <= 16) JQ_R(16);
+  else if (sl <= 32) JQ_R(32);
+  else JQ_R(64);
+#undef JQ_R
   return jqh::launch_status();
 }
 
@@ -288,8 +458,14 @@ int jq_gather_qmm(const void* x, int x_dtype, int64_t x_batch, int64_t M, const 
   (void)sorted_indices;  // grouping is done on the device in every case
   const int64_t Nv[1] = {N}, Kv[1] = {K};
   const Choice c = choose(n_pairs * M, E, n_pairs, group_size, x_dtype, sb_dtype, 1, &bits, Nv, Kv);
-  s = build_plan(rhs, n_pairs, E, M, c.tile_rows, workspace, plan, lhs, st);
-  if (s) return s;
+  // One row per tile on the vector-ALU kernel: the pairs are the tiles, no grouping needed.
+  const bool direct = c.k == Kern::gemv && c.tile_rows == 1 && M == 1;
+  if (direct) {
+    plan = direct_plan(rhs, n_pairs, E, lhs);
+  } else {
+    s = build_plan(rhs, n_pairs, E, M, c.tile_rows, workspace, plan, lhs, st);
+    if (s) return s;
+  }
   plan.x_rows = x_batch * M;
   jqk::QmmProblem p;
   p.x = x;
@@ -302,7 +478,7 @@ int jq_gather_qmm(const void* x, int x_dtype, int64_t x_batch, int64_t M, const 
   p.K = K;
   p.expert_stride_codes = N * (K * bits / 32);
   p.expert_stride_sb = N * (K / group_size);
-  const int64_t mt = max_tiles_for(n_pairs, E, M, c.tile_rows);
+  const int64_t mt = direct ? n_pairs : max_tiles_for(n_pairs, E, M, c.tile_rows);
   return grouped_launch(c, p, nullptr, plan, mt, bits, group_size, x_dtype, sb_dtype, y_dtype, st);
 }
 
@@ -335,8 +511,13 @@ int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, i
   const int64_t Nv[2] = {I, H}, Kv[2] = {H, I};
   const Choice c = choose(n_pairs, E, n_pairs, group_size, x_dtype, sb_dtype, 2, bv, Nv, Kv);
   jqk::GatherPlan plan;
-  s = build_plan(idx, n_pairs, E, 1, c.tile_rows, workspace, plan, nullptr, st);
-  if (s) return s;
+  const bool direct = c.k == Kern::gemv && c.tile_rows == 1;
+  if (direct) {
+    plan = direct_plan(idx, n_pairs, E, nullptr);
+  } else {
+    s = build_plan(idx, n_pairs, E, 1, c.tile_rows, workspace, plan, nullptr, st);
+    if (s) return s;
+  }
   jqk::GatherPlan plan_gu = plan;
   plan_gu.lhs = nullptr;
   plan_gu.pair_div = k;  // x row = pair / k
@@ -349,7 +530,7 @@ int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, i
   g.expert_stride_sb = I * (H / group_size);
   u = g;
   u.codes = up_codes; u.scales = up_scales; u.biases = up_biases;
-  const int64_t mt = max_tiles_for(n_pairs, E, 1, c.tile_rows);
+  const int64_t mt = direct ? n_pairs : max_tiles_for(n_pairs, E, 1, c.tile_rows);
   s = grouped_launch(c, g, &u, plan_gu, mt, bits_gu, group_size, x_dtype, sb_dtype, y_dtype, st);
   if (s) return s;
   d.x = h_buf; d.codes = down_codes; d.scales = down_scales; d.biases = down_biases; d.y = out;

@@ -50,6 +50,13 @@ struct GatherPlan {
   int M;                     // rows per pair
   int pair_div;              // without lhs: x row of pair p is p / pair_div
   int64_t x_rows;            // rows of x; a pair mapping outside reads zeros
+  // Direct tiles (tiles == NULL; vector-ALU gather GEMV only, M == 1): tile t holds pairs
+  // [t*direct_rows, t*direct_rows + direct_rows) of expert rhs[t*direct_rows] (expert 0 when
+  // rhs is NULL; with rhs, direct_rows is 1); an id >= E reads nothing and is not stored.
+  const uint32_t* rhs;
+  int E;
+  int direct_pairs;
+  int direct_rows;
 };
 
 struct QmmProblem {

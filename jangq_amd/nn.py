@@ -115,12 +115,9 @@ class SharedExpertMLP(torch.nn.Module):
         self.down_proj = QuantizedLinear(hidden, dims, **kw)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        g, u = ops.quantized_matmul_multi(x, [
-            (self.gate_proj.weight, self.gate_proj.scales, self.gate_proj.biases,
-             self.gate_proj.group_size, self.gate_proj.bits),
-            (self.up_proj.weight, self.up_proj.scales, self.up_proj.biases,
-             self.up_proj.group_size, self.up_proj.bits)])
-        h = (torch.nn.functional.silu(g.float()) * u.float()).to(x.dtype)
+        g, u = self.gate_proj, self.up_proj
+        h = ops.quantized_swiglu(x, (g.weight, g.scales, g.biases, g.bits),
+                                 (u.weight, u.scales, u.biases, u.bits), g.group_size)
         return self.down_proj(h)
 
 
@@ -151,7 +148,6 @@ class SparseMoeBlock(torch.nn.Module):
             logits = self.gate(x).float()
         inds, scores = ops.moe_route(logits, self.top_k, self.norm_topk_prob)
         y = self.switch_mlp(x, inds)
-        y = (y.float() * scores.unsqueeze(-1)).sum(dim=-2).to(x.dtype)
-        if self.shared_expert is not None:
-            y = y + self.shared_expert(x)
-        return y
+        shared = self.shared_expert(x) if self.shared_expert is not None else None
+        # (y * scores[..., None]).sum(-2) (+ shared), qwen4_exp/modeling.py:594-597
+        return ops.moe_combine(y, scores, shared)

@@ -317,3 +317,53 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, down, group_siz
         _ptr(h), _ptr(out), _dtype_code(out, "output"), _ptr(ws), ws.numel(), _stream()),
         "switch_glu")
     return out
+
+
+def moe_combine(y: torch.Tensor, weights: torch.Tensor,
+                shared: torch.Tensor | None = None) -> torch.Tensor:
+    """sum_j weights[..., j] * y[..., j, :] in fp32 (slot order), in y.dtype, plus ``shared``
+    (rounded again): one launch for ``(y * scores[..., None]).sum(-2) (+ shared_expert(x))``
+    of qwen4_exp/modeling.py:594-597."""
+    y = _dev(y, "expert outputs")
+    w = _dev(weights, "weights")
+    if w.dtype != torch.float32:
+        w = w.float().contiguous()
+    k, H = y.shape[-2], y.shape[-1]
+    lead = tuple(y.shape[:-2])
+    if tuple(w.shape) != (*lead, k):
+        raise ValueError(f"weights must be {(*lead, k)}, got {tuple(w.shape)}")
+    T = math.prod(lead)
+    if shared is not None:
+        shared = _dev(shared, "shared")
+        if tuple(shared.shape) != (*lead, H) or shared.dtype != y.dtype:
+            raise ValueError("shared must match the combined output's shape and dtype")
+    out = torch.empty((*lead, H), dtype=y.dtype, device=y.device)
+    _lib.check(_lib.lib().jq_moe_combine(_ptr(y), _ptr(w), _ptr(shared), T, k, H, _ptr(out),
+                                         _dtype_code(y, "expert outputs"), _stream()),
+               "moe_combine")
+    return out
+
+
+def quantized_swiglu(x: torch.Tensor, gate, up, group_size: int = 64) -> torch.Tensor:
+    """silu(gate(x)) * up(x) of a dense MLP, each projection rounded to x.dtype first; gate and
+    up are (w, scales, biases, bits) with the same bits, N and K. One launch at decode sizes."""
+    x = _dev(x, "x")
+    gw, gsc, gb, bits = gate
+    uw, usc, ub, bits_u = up
+    if bits_u != bits:
+        raise ValueError("gate and up projections must share a bit width")
+    _check_bits_gs(bits, group_size)
+    gw, uw = _codes(gw), _codes(uw)
+    N, K = gw.shape[0], packed_in_features(gw, bits)
+    if tuple(uw.shape) != tuple(gw.shape) or x.shape[-1] != K:
+        raise ValueError("gate / up / x shapes do not match")
+    M = math.prod(x.shape[:-1])
+    h = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
+    decode = M <= (2 if bits == 2 else 4)
+    up_buf = None if decode else torch.empty_like(h)
+    _lib.check(_lib.lib().jq_quantized_swiglu(
+        _ptr(x), _dtype_code(x, "x"), M, N, K, _ptr(gw), _ptr(_dev(gsc, "scales")),
+        _ptr(_dev(gb, "biases")), _ptr(uw), _ptr(_dev(usc, "scales")), _ptr(_dev(ub, "biases")),
+        _dtype_code(gsc, "scales"), bits, group_size, _ptr(h), _ptr(up_buf),
+        _dtype_code(h, "output"), _stream()), "quantized_swiglu")
+    return h

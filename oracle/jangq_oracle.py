@@ -240,6 +240,26 @@ def switch_glu(x_f32, idx, gate, up, down, group_size: int, out_dtype: str = "bf
     return out, hs
 
 
+def moe_combine(y, w, shared=None, out_dtype: str = "bf16") -> np.ndarray:
+    """The caller-side combine of jang-tools/jang_tools/qwen4_exp/modeling.py:594-597:
+    round((y * w[..., None]).sum(-2)) (+ shared, rounded again); y [T, k, H] values of
+    out_dtype, w [T, k]. Products and the slot-order sum in fp64."""
+    y = np.asarray(y, dtype=np.float64)
+    w = np.asarray(w, dtype=np.float64)
+    r = round_to((y * w[..., None]).sum(-2), out_dtype)
+    if shared is not None:
+        r = round_to(r.astype(np.float64) + np.asarray(shared, dtype=np.float64), out_dtype)
+    return r
+
+
+def swiglu_pair(x_f32, gate, up, group_size: int, out_dtype: str = "bf16") -> np.ndarray:
+    """h = round(silu(round(x @ Wg^T)) * round(x @ Wu^T)) of a dense MLP (the shared expert of
+    qwen4_exp/modeling.py:597; gate/up = (w, s_f32, b_f32, bits)), matmuls in fp64."""
+    g = round_to(quantized_matmul(x_f32, *gate[:3], gate[3], group_size), out_dtype)
+    u = round_to(quantized_matmul(x_f32, *up[:3], up[3], group_size), out_dtype)
+    return round_to(silu(g) * u.astype(np.float64), out_dtype)
+
+
 def route_topk(logits, k: int, renorm: bool = True):
     """softmax in fp64, top-k by descending probability (ties: lower id first)."""
     z = np.asarray(logits, dtype=np.float64)

@@ -109,9 +109,11 @@ def test_switch_glu(T, k, E, bits_gu, bits_d):
     assert_close(values_of(out), ref, f"switch_glu T{T} k{k}")
 
 
-def test_moe_block_module():
-    """Router (8-bit gate) -> top-k -> SwitchGLU -> weighted sum + shared expert."""
-    H, I, E, k, T = 256, 128, 16, 4, 5
+@pytest.mark.parametrize("T", [1, 5])
+def test_moe_block_module(T):
+    """Router (8-bit gate) -> top-k -> SwitchGLU -> weighted sum + shared expert (decode-size
+    fused SwiGLU at T = 1, grouped dense launch at T = 5)."""
+    H, I, E, k = 256, 128, 16, 4
     blk = jnn.SparseMoeBlock(H, I, E, k, shared_hidden=256, bits=2, device="cuda")
     rng = np.random.default_rng(0)
     ws = {}
@@ -138,3 +140,64 @@ def test_moe_block_module():
     h = O.round_bf16(O.silu(g) * u)
     shared = O.round_bf16(O.quantized_matmul(h, sh[2].packed, sh[2].s, sh[2].b, 8, 64))
     assert_close(values_of(y), O.round_bf16(routed + shared), "moe block")
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("T,k,H", [(1, 4, 4096), (32, 10, 4096), (3, 2, 100)])
+def test_moe_combine(dt, T, k, H):
+    """One-launch combine against the caller composition (oracle), with and without the
+    shared expert's output; H = 100 takes the unvectorised kernel."""
+    rng = np.random.default_rng(T * 3 + k)
+    y = O.round_to(rng.standard_normal((T, k, H), dtype=np.float32), dt)
+    w = rng.random((T, k)).astype(np.float32)
+    sh = O.round_to(rng.standard_normal((T, H), dtype=np.float32), dt)
+    ty, tw, tsh = to_tensor(y, dt), torch.from_numpy(w).cuda(), to_tensor(sh, dt)
+    for shared in (None, tsh):
+        got = values_of(jq.moe_combine(ty, tw, shared))
+        ref = O.moe_combine(y, w, None if shared is None else sh, dt)
+        if dt == "f32":
+            np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
+        else:
+            assert_close(got, ref, f"combine {dt} T{T} k{k}")
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 9])
+def test_quantized_swiglu(bits, M):
+    """Dense SwiGLU pair: one gathered launch at decode sizes (M <= 4; 2-bit M <= 2), the
+    grouped dense launch + elementwise kernel above."""
+    N, K, gs = 200, 512, 64
+    g = QWeight(N, K, bits, gs, seed=bits * 3)
+    u = QWeight(N, K, bits, gs, seed=bits * 3 + 1)
+    rng = np.random.default_rng(M + bits)
+    x = O.round_bf16(rng.standard_normal((M, K), dtype=np.float32))
+    h = jq.quantized_swiglu(to_tensor(x, "bf16"), (g.dw, g.ds, g.db, bits), (u.dw, u.ds, u.db, bits), gs)
+    ref = O.swiglu_pair(x, (g.packed, g.s, g.b, bits), (u.packed, u.s, u.b, bits), gs)
+    assert tuple(h.shape) == (M, N)
+    assert_close(values_of(h), ref, f"swiglu b{bits} M{M}")
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 4, 128), (1, 10, 512), (2, 8, 64)])
+def test_switch_glu_direct_pairs(T, k, E):
+    """Decode routing (every pair its own expert tile, no plan kernel) at the configs' expert
+    counts, with repeated experts across tokens."""
+    H, I, gs = 512, 256, 128
+    g = _stack(E, I, H, 2, gs, seed=31)
+    u = _stack(E, I, H, 2, gs, seed=32)
+    d = _stack(E, H, I, 2, gs, seed=33)
+    rng = np.random.default_rng(E + k)
+    x = O.round_bf16(rng.standard_normal((T, H), dtype=np.float32))
+    inds = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    if T > 1:
+        inds[1, 0] = inds[0, 0]
+    out = jq.switch_glu(to_tensor(x, "bf16"), torch.from_numpy(inds).cuda(),
+                        (g.dw, g.ds, g.db, 2), (u.dw, u.ds, u.db, 2), (d.dw, d.ds, d.db, 2), gs)
+    ref, _ = O.switch_glu(x, inds, (g.packed, g.s, g.b, 2), (u.packed, u.s, u.b, 2),
+                          (d.packed, d.s, d.b, 2), gs, "bf16")
+    assert_close(values_of(out), ref, f"switch_glu direct T{T} k{k} E{E}")
+    # gather_qmm of the same pairs (one row each) also runs without a plan
+    y = jq.gather_qmm(to_tensor(x, "bf16")[:, None, None, :], g.dw, g.ds, g.db,
+                      rhs_indices=torch.from_numpy(inds).cuda(), group_size=gs, bits=2)
+    lhs = np.repeat(np.arange(T), k)
+    refg = O.gather_qmm(x[:, None, :], g.packed, g.s, g.b, lhs, inds.reshape(-1), 2, gs)
+    assert_close(values_of(y).reshape(T * k, 1, I), O.round_bf16(refg), "gather direct")

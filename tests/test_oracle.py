@@ -326,3 +326,43 @@ def test_half_ulp_helper():
     # a bf16 rounding of any value stays within the allowance
     r = np.random.default_rng(0).standard_normal(1000).astype(np.float32) * 50
     assert np.all(np.abs(O.round_bf16(r) - r) <= half_ulp(r, "bf16"))
+
+
+def test_moe_combine_vs_torch_composition():
+    """The oracle's combine equals the array composition the reference's caller writes,
+    (y * scores[..., None]).sum(-2) then + shared (qwen4_exp/modeling.py:594-597), evaluated
+    with torch on the CPU in fp64 and rounded to bf16 at the same two points."""
+    import torch
+
+    rng = np.random.default_rng(41)
+    T, k, H = 3, 5, 64
+    y = O.round_bf16(rng.standard_normal((T, k, H), dtype=np.float32))
+    w = rng.random((T, k)).astype(np.float32)
+    sh = O.round_bf16(rng.standard_normal((T, H), dtype=np.float32))
+    ty = torch.from_numpy(y).double()
+    routed = (ty * torch.from_numpy(w).double().unsqueeze(-1)).sum(dim=-2).to(torch.bfloat16)
+    ref = (routed.double() + torch.from_numpy(sh).double()).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(O.moe_combine(y, w, sh), ref)
+    np.testing.assert_array_equal(O.moe_combine(y, w), routed.float().numpy())
+    # one-hot weights select a slot exactly
+    onehot = np.zeros((T, k), np.float32)
+    onehot[:, 2] = 1.0
+    np.testing.assert_array_equal(O.moe_combine(y, onehot), y[:, 2, :])
+
+
+def test_swiglu_pair_equals_switch_glu_single_expert():
+    """A dense SwiGLU pair is SwitchGLU's gate/up stage over a one-expert stack."""
+    rng = np.random.default_rng(43)
+    H, I, T = 128, 64, 3
+    mats = []
+    for seed in (1, 2, 3):
+        r = np.random.default_rng(seed)
+        rows, cols = (I, H) if seed < 3 else (H, I)
+        ww = O.round_bf16(r.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02))
+        p, s, b, _ = O.quantize_affine(ww, 4, 64)
+        mats.append((p, O.sidecar_f32(s, "bf16"), O.sidecar_f32(b, "bf16"), 4))
+    x = O.round_bf16(rng.standard_normal((T, H), dtype=np.float32))
+    h = O.swiglu_pair(x, mats[0], mats[1], 64)
+    stack = [(m[0][None], m[1][None], m[2][None], m[3]) for m in mats]
+    _, hs = O.switch_glu(x, np.zeros((T, 1), np.int64), *stack, 64, "bf16")
+    np.testing.assert_array_equal(h, hs[:, 0, :])
