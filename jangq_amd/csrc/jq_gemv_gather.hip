@@ -85,12 +85,34 @@ JQ_DEV int4 get_tile(const GatherPlan& pl, int t) {
   return make_int4(ok ? (int)e : 0, 0, ok ? (left < pl.direct_rows ? left : pl.direct_rows) : 0, r0);
 }
 
-template <class D, int SB, int MT, int RB, int NB>
+// Sum over each group of 64/RW consecutive lanes; the total lands in the group's last lane
+// (RW = 1: the whole wave, lane 63).
+template <int RW>
+JQ_DEV float group_total(float v) {
+  if constexpr (RW == 1) {
+    return wave_total_lane63(v);
+  } else {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false));  // row_ror 4
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));  // row_ror 8
+    if constexpr (RW == 2)
+      v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false));  // row_bcast 15
+    return v;
+  }
+}
+
+// RW: rows per wave instruction. Rows shorter than 64 lane chunks (RW = 2, 4) split a single
+// wave into RW groups of 64/RW lanes; group g loads item rows g*RBL .. g*RBL + RBL - 1, and a
+// lane keeps the activations of its chunk for every row. RBL: ring slots (rows) per lane.
+template <class D, int SB, int MT, int RBL, int NB, int RW>
 __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs a) {
   constexpr int BITS = D::BITS;
   constexpr int UPL = units_per_chunk<BITS>();
   constexpr int NW = BITS * UPL;
+  constexpr int RB = RBL * RW;   // rows of an item (both projections)
   constexpr int ROWS = RB / NB;  // weight rows of one projection per item
+  constexpr int CL = 64 / RW;    // lanes per row group
   __shared__ float red[2][kMaxWaves][RB * MT];
 
   const int ntiles = a.plan.n_tiles ? *a.plan.n_tiles
@@ -110,8 +132,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
   const uint32_t rowbytes = (uint32_t)(K / 32) * BITS * 4;
   const uint32_t sbrow = (uint32_t)(K >> (a.ushift + 5)) * 2;
 
-  const int c = wave * CW + lane;
-  const bool act = lane < CW && c < C;
+  const int sr = RW == 1 ? 0 : lane / CL;  // row group of the lane
+  const int lc = RW == 1 ? lane : lane % CL;
+  const int c = wave * CW + lc;
+  const bool act = lc < CW && c < C;
   const int ci = act ? c : 0;
   const uint32_t voff = (uint32_t)ci * (4 * NW);
   uint32_t vsb[UPL];
@@ -134,10 +158,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
       rb[q] = make_rsrc((const char*)pb.biases + sb0, rows * sbrow);
     }
   };
-  // Ring slot r holds row r / NB of projection r % NB.
+  // Ring slot r of a lane holds item row ir = sr*RBL + r: row ir / NB of projection r % NB.
   auto load_row = [&](const Rsrc (&rc)[NB], const Rsrc (&rs)[NB], const Rsrc (&rb)[NB], int r,
                       RowSlot<NW, UPL>& slot) {
-    const int q = r % NB, rr = r / NB;
+    const int q = r % NB, rr = (sr * RBL + r) / NB;
     load_chunk<NW>(rc[q], voff + rr * rowbytes, slot.w);
 #pragma unroll
     for (int t = 0; t < UPL; ++t) {
@@ -175,9 +199,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
   int64_t row0 = (int64_t)rbi * ROWS;
   Rsrc rc[NB], rs[NB], rbv[NB];
   views(tl, row0, true, rc, rs, rbv);
-  RowSlot<NW, UPL> ring[RB];
+  RowSlot<NW, UPL> ring[RBL];
 #pragma unroll
-  for (int r = 0; r < RB; ++r) {
+  for (int r = 0; r < RBL; ++r) {
     load_row(rc, rs, rbv, r, ring[r]);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
@@ -195,9 +219,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
     Rsrc rc2[NB], rs2[NB], rb2[NB];
     views(tl2, row02, more, rc2, rs2, rb2);
 
-    float acc[RB][MT];
+    float acc[RBL][MT];
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
+    for (int r = 0; r < RBL; ++r) {
 #pragma unroll
       for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
 #pragma unroll
@@ -218,11 +242,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
     }
 
 #pragma unroll
-    for (int r = 0; r < RB; ++r)
+    for (int r = 0; r < RBL; ++r)
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        const float v = wave_total_lane63(acc[r][m]);
-        if (lane == 63) red[par][wave][r * MT + m] = v;
+        const float v = group_total<RW>(acc[r][m]);
+        if (lc == CL - 1) red[par][wave][(sr * RBL + r) * MT + m] = v;
       }
     __syncthreads();
     if (wave == 0 && lane < ROWS * MT) {
@@ -261,20 +285,20 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
   }
 }
 
-template <class D, int SB, int MT, int RB, int NB>
+template <class D, int SB, int MT, int RBL, int NB, int RW>
 int launch_g(GatherArgs& a, int64_t max_tiles, hipStream_t st) {
   int kws = 0;
-  const int kw = gemv_waves(a.p[0].K, D::BITS, &kws);
+  const int kw = RW == 1 ? gemv_waves(a.p[0].K, D::BITS, &kws) : 1;
   if (kw > kMaxWaves) return JQ_ERR_SHAPE;
   a.kwshift = kws;
-  constexpr int ROWS = RB / NB;
+  constexpr int ROWS = RBL * RW / NB;
   const int64_t nrb = (a.p[0].N + ROWS - 1) / ROWS;
   const int64_t max_items = max_tiles * nrb;
   if (nrb == 0 || max_items == 0) return JQ_OK;
   if (max_items >= ((int64_t)1 << 31)) return JQ_ERR_SHAPE;
   a.nrb = (int)nrb;
   int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_gather_kernel<D, SB, MT, RB, NB>,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_gather_kernel<D, SB, MT, RBL, NB, RW>,
                                                    64 * kw, 0) != hipSuccess || nb < 1)
     nb = 1;
   int dev = 0, cus = 256;
@@ -283,20 +307,29 @@ int launch_g(GatherArgs& a, int64_t max_tiles, hipStream_t st) {
     cus = 256;
   const int64_t cap = (int64_t)nb * cus;
   const int grid = (int)(max_items < cap ? max_items : cap);
-  gemv_gather_kernel<D, SB, MT, RB, NB><<<grid, 64 * kw, 0, st>>>(a);
+  gemv_gather_kernel<D, SB, MT, RBL, NB, RW><<<grid, 64 * kw, 0, st>>>(a);
   return jqh::launch_status();
 }
 
-// Rows in flight per lane: 4 rows of one projection, or 4 rows each of gate and up.
-template <class D, int SB, int NB>
-int launch_mt(GatherArgs& a, int mt, int64_t max_tiles, hipStream_t st) {
-  constexpr int RB = 4 * NB;
-  if (mt == 1) return launch_g<D, SB, 1, RB, NB>(a, max_tiles, st);
-  if (mt == 2) return launch_g<D, SB, 2, RB, NB>(a, max_tiles, st);
+// Rows in flight per lane: 4 rows of one projection, or 4 rows each of gate and up; rows of
+// at most 16 (32) lane chunks take 4 (2) rows per wave instruction.
+template <class D, int SB, int NB, int RW>
+int launch_rw(GatherArgs& a, int mt, int64_t max_tiles, hipStream_t st) {
+  constexpr int RBL = 4 * NB;
+  if (mt == 1) return launch_g<D, SB, 1, RBL, NB, RW>(a, max_tiles, st);
+  if (mt == 2) return launch_g<D, SB, 2, RBL, NB, RW>(a, max_tiles, st);
   if constexpr (D::BITS != 2) {
-    if (mt == 4) return launch_g<D, SB, 4, RB, NB>(a, max_tiles, st);
+    if (mt == 4) return launch_g<D, SB, 4, RBL, NB, RW>(a, max_tiles, st);
   }
   return JQ_ERR_SHAPE;
+}
+
+template <class D, int SB, int NB>
+int launch_mt(GatherArgs& a, int mt, int64_t max_tiles, hipStream_t st) {
+  const int64_t C = a.p[0].K / (32 * units_per_chunk<D::BITS>());  // lane chunks per row
+  if (C <= 16) return launch_rw<D, SB, NB, 4>(a, mt, max_tiles, st);
+  if (C <= 32) return launch_rw<D, SB, NB, 2>(a, mt, max_tiles, st);
+  return launch_rw<D, SB, NB, 1>(a, mt, max_tiles, st);
 }
 
 template <int BITS, int XDT, int NB>

@@ -23,6 +23,29 @@ constexpr int kGemmTileRows = 16;
 constexpr int64_t kGemvRows = 4096;
 constexpr int kMaxExperts = 4096;
 
+// One step of the wave argmax: (v, id) against the DPP-moved (v, id) of another lane (lanes
+// outside row_mask keep theirs); larger value wins, ties go to the lower id.
+template <int CTRL, int ROWS>
+JQ_DEV void argmax_step(float& v, int& id) {
+  const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+      __builtin_bit_cast(int, -INFINITY), __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false));
+  const int oid = __builtin_amdgcn_update_dpp(0x7FFFFFFF, id, CTRL, ROWS, 0xF, false);
+  if (ov > v || (ov == v && oid < id)) { v = ov; id = oid; }
+}
+
+// Wave-wide argmax of (v, id), broadcast to every lane: DPP row operations carry the maximum
+// into lane 63 (as a wave sum would), a scalar read hands it to all lanes.
+JQ_DEV void wave_argmax(float& v, int& id) {
+  argmax_step<0xB1, 0xF>(v, id);   // quad_perm 1,0,3,2
+  argmax_step<0x4E, 0xF>(v, id);   // quad_perm 2,3,0,1
+  argmax_step<0x124, 0xF>(v, id);  // row_ror 4
+  argmax_step<0x128, 0xF>(v, id);  // row_ror 8
+  argmax_step<0x142, 0xA>(v, id);  // row_bcast 15
+  argmax_step<0x143, 0xC>(v, id);  // row_bcast 31
+  v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+  id = __builtin_amdgcn_readlane(id, 63);
+}
+
 // One wave per token. Lane l holds logits l, l + 64, ... (SL = ceil(E/64) of them) in
 // registers; top-k by k rounds of wave argmax (ties -> lowest expert id), probabilities from a
 // max-subtracted fp32 softmax.
@@ -67,12 +90,7 @@ __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ lo
       const int e = lane + 64 * i;
       if (!taken[i] && (v[i] > best || (v[i] == best && e < bid))) { best = v[i]; bid = e; }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(best, o, 64);
-      const int oid = __shfl_xor(bid, o, 64);
-      if (ov > best || (ov == best && oid < bid)) { best = ov; bid = oid; }
-    }
+    wave_argmax(best, bid);
 #pragma unroll
     for (int i = 0; i < SL; ++i)
       if (lane + 64 * i == bid) taken[i] = true;
