@@ -88,6 +88,17 @@ int jq_quantize(const void* w, int w_dtype, int bits, int group_size, int64_t ro
                 jq_stream_t stream);
 
 /*
+ * Lossless expansion of 1-bit storage codes to 2-bit runtime codes: `words` uint32 words of an
+ * LSB-first 1-bit stream (32 codes each) become 2*words words of the 2-bit stream of the same
+ * codes (scales and biases are unchanged). Rows stay rows: a [rows, K/32] 1-bit matrix becomes
+ * [rows, K/16].
+ * Replaces jang-tools/jang_tools/affine.py:402-416 (expand_packed_1bit_to_2bit_numpy / _mlx),
+ * applied per shard at load time by affine.py:527-544.
+ */
+int jq_expand_1bit_to_2bit(const uint32_t* src, int64_t words, uint32_t* dst,
+                           jq_stream_t stream);
+
+/*
  * y[M, N] = x[M, K] @ dequant(W)[N, K]^T  (transpose=True), fp32 accumulation.
  * x_dtype: JQ_BF16 / JQ_F16 / JQ_F32; y_dtype likewise (MLX returns x.dtype).
  * Replaces mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits) as

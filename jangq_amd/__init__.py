@@ -7,6 +7,8 @@ HIP kernels of ``libjangq_amd.so`` (C ABI: ``include/jangq_amd.h``).
 """
 from .ops import (  # noqa: F401
     dequantize,
+    dequantize_tensor,
+    expand_packed_1bit_to_2bit,
     gather_qmm,
     moe_combine,
     moe_route,
@@ -21,7 +23,7 @@ from ._lib import JangqError  # noqa: F401
 from .shapes import bit_inference, infer_bits_group_size  # noqa: F401
 
 __all__ = [
-    "dequantize", "gather_qmm", "moe_combine", "moe_route", "quantize", "quantized_matmul",
+    "dequantize", "dequantize_tensor", "expand_packed_1bit_to_2bit", "gather_qmm", "moe_combine", "moe_route", "quantize", "quantized_matmul",
     "quantized_matmul_multi", "quantized_swiglu", "switch_glu", "unpack", "bit_inference", "infer_bits_group_size",
     "JangqError",
 ]

@@ -201,9 +201,46 @@ int launch_quant(const void* w, int wd, int gs, int64_t groups, uint32_t* c, voi
 
 inline int gs_shift(int gs) { return gs == 32 ? 5 : gs == 64 ? 6 : 7; }
 
+// 1-bit storage codes -> 2-bit runtime codes, losslessly (reference
+// jang-tools/jang_tools/affine.py:402-416): code i of a source word (bit i) becomes the 2-bit
+// field i of the destination stream, i.e. bit 2i of destination word 2w + i/16. Each thread
+// spreads one source word: its low and high halves each go to the even bits of one word.
+JQ_DEV uint32_t spread_even_bits(uint32_t h) {  // bits 0..15 of h -> bits 0, 2, ..., 30
+  h &= 0xFFFFu;
+  h = (h | (h << 8)) & 0x00FF00FFu;
+  h = (h | (h << 4)) & 0x0F0F0F0Fu;
+  h = (h | (h << 2)) & 0x33333333u;
+  h = (h | (h << 1)) & 0x55555555u;
+  return h;
+}
+
+__global__ void __launch_bounds__(256) expand1to2_kernel(const uint32_t* __restrict__ src,
+                                                         int64_t words,
+                                                         uint32_t* __restrict__ dst) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < words;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const uint32_t v = src[i];
+    uint2 o;
+    o.x = spread_even_bits(v);
+    o.y = spread_even_bits(v >> 16);
+    *(uint2*)(dst + 2 * i) = o;
+  }
+}
+
 }  // namespace
 
 extern "C" {
+
+int jq_expand_1bit_to_2bit(const uint32_t* src, int64_t words, uint32_t* dst,
+                           jq_stream_t stream) {
+  if (words < 0) return JQ_ERR_SHAPE;
+  if (words == 0) return JQ_OK;
+  if (!src || !dst) return JQ_ERR_NULL;
+  const int64_t blocks = (words + 255) / 256;
+  expand1to2_kernel<<<(unsigned)(blocks < 16384 ? blocks : 16384), 256, 0, (hipStream_t)stream>>>(
+      src, words, dst);
+  return jqh::launch_status();
+}
 
 int jq_abi_version(void) { return JQ_ABI_VERSION; }
 

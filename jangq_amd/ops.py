@@ -367,3 +367,43 @@ def quantized_swiglu(x: torch.Tensor, gate, up, group_size: int = 64) -> torch.T
         _dtype_code(gsc, "scales"), bits, group_size, _ptr(h), _ptr(up_buf),
         _dtype_code(h, "output"), _stream()), "quantized_swiglu")
     return h
+
+
+def expand_packed_1bit_to_2bit(w: torch.Tensor) -> torch.Tensor:
+    """1-bit storage codes [..., P] (uint32) -> the same codes as 2-bit runtime codes
+    [..., 2P]; scales and biases are unchanged (affine.py:402-416, lossless)."""
+    w = _codes(w)
+    out = torch.empty((*w.shape[:-1], 2 * w.shape[-1]), dtype=torch.int32, device=w.device)
+    _lib.check(_lib.lib().jq_expand_1bit_to_2bit(_ptr(w), w.numel(), _ptr(out), _stream()),
+               "expand_packed_1bit_to_2bit")
+    return out.view(torch.uint32)
+
+
+def dequantize_tensor(qweight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                      bits: int, shape, block_size: int = 64) -> torch.Tensor:
+    """Dequantize a flat (v1) JANG tensor to fp32 (quantize.py:292-326): the codes of all
+    blocks form one LSB-first stream (uint8 ``qweight``), block b covers flat elements
+    [b*block_size, (b+1)*block_size) and uses scales[b], biases[b]; the result is cut to
+    prod(shape) elements. Every block is a whole number of 32-bit words, so the stream is the
+    row layout of a [n_blocks, block_size] matrix and runs on the row dequant kernel."""
+    _check_bits_gs(bits, block_size)
+    scales = _dev(scales, "scales").reshape(-1, 1)
+    biases = _dev(biases, "biases").reshape(-1, 1)
+    n_blocks = scales.shape[0]
+    if biases.shape[0] != n_blocks or scales.dtype != biases.dtype:
+        raise ValueError("scales and biases must be [n_blocks] of one dtype")
+    total = math.prod(shape)
+    if total > n_blocks * block_size:
+        raise ValueError(f"shape {tuple(shape)} needs more than {n_blocks} blocks")
+    nbytes = n_blocks * block_size * bits // 8
+    q = _dev(qweight, "qweight").reshape(-1)
+    if q.dtype != torch.uint8:
+        raise ValueError("qweight must be the uint8 code stream")
+    if q.numel() < nbytes:
+        raise ValueError(f"qweight holds {q.numel()} bytes, the blocks need {nbytes}")
+    words = q[:nbytes].view(torch.int32) if q.data_ptr() % 16 == 0 else q[:nbytes].clone().view(torch.int32)
+    out = torch.empty((n_blocks, block_size), dtype=torch.float32, device=q.device)
+    _lib.check(_lib.lib().jq_dequantize(
+        _ptr(words), _ptr(scales), _ptr(biases), _dtype_code(scales, "scales"), bits, block_size,
+        n_blocks, block_size, _ptr(out), JQ_F32, _stream()), "dequantize_tensor")
+    return out.reshape(-1)[:total].reshape(tuple(shape))

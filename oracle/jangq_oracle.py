@@ -181,6 +181,31 @@ def dequantize_affine(w, scales_f32, biases_f32, bits: int, group_size: int) -> 
 # ----------------------------------------------------------------------------- matmuls
 
 
+def dequantize_tensor_flat(qweight_u8, scales, biases, bits: int, shape,
+                           block_size: int = 64) -> np.ndarray:
+    """Flat (v1) dequant of jang-tools/jang_tools/quantize.py:292-326: unpack the whole
+    LSB-first stream (n_blocks * block_size codes), q * s + b per block in fp32 (two roundings),
+    cut to prod(shape) elements."""
+    s = np.asarray(scales).astype(np.float32).reshape(-1)
+    b = np.asarray(biases).astype(np.float32).reshape(-1)
+    n_blocks = s.size
+    q = unpack_bits(np.asarray(qweight_u8, np.uint8), bits, n_blocks * block_size)
+    q = q.reshape(n_blocks, block_size).astype(np.float32)
+    out = (q * s[:, None]).astype(np.float32) + b[:, None]
+    total = int(np.prod(shape))
+    return out.reshape(-1)[:total].reshape(tuple(shape))
+
+
+def expand_1bit_to_2bit(packed) -> np.ndarray:
+    """1-bit -> 2-bit code expansion (jang-tools/jang_tools/affine.py:402-416), restated
+    through the code stream: the 1-bit codes of each row, repacked at 2 bits."""
+    w = np.asarray(packed, dtype=np.uint32)
+    flat = w.reshape(-1, w.shape[-1])
+    out = np.stack([pack_bits(unpack_bits(r.view(np.uint8), 1, 32 * r.size), 2).view(np.uint32)
+                    for r in flat])
+    return out.reshape(*w.shape[:-1], 2 * w.shape[-1])
+
+
 def quantized_matmul(x_f32, w, s_f32, b_f32, bits: int, group_size: int) -> np.ndarray:
     """y = x @ dequant(W)^T accumulated in fp64 (x given as fp32 values). Returns fp64."""
     W = dequantize_affine(w, s_f32, b_f32, bits, group_size).astype(np.float64)

@@ -88,3 +88,40 @@ def test_quantize_dequantize_roundtrip_full_size():
     packed, s_ref, b_ref, _ = O.quantize_affine(w, 4, 64, sidecar="bf16")
     ref = O.dequantize_affine(packed, O.sidecar_f32(s_ref, "bf16"), O.sidecar_f32(b_ref, "bf16"), 4, 64)
     assert np.array_equal(values_of(deq), ref)
+
+
+@pytest.mark.parametrize("rows,P", [(1, 1), (37, 5), (4096, 64)])
+def test_expand_1bit_to_2bit(rows, P):
+    """1-bit storage -> 2-bit runtime codes (affine.py:402-416): bit-exact, and the expanded
+    codes dequantize to the 1-bit values q*s + b with the same sidecars."""
+    rng = np.random.default_rng(rows + P)
+    w = rng.integers(0, 2**32, size=(rows, P), dtype=np.uint64).astype(np.uint32)
+    got = jq.expand_packed_1bit_to_2bit(codes_tensor(w))
+    assert tuple(got.shape) == (rows, 2 * P)
+    np.testing.assert_array_equal(got.view(torch.int32).cpu().numpy().view(np.uint32),
+                                  O.expand_1bit_to_2bit(w))
+    if rows == 37:
+        K = 32 * P
+        s = (rng.random((rows, K // 32)) * 0.1).astype(np.float32)
+        b = (rng.standard_normal((rows, K // 32)) * 0.1).astype(np.float32)
+        deq = jq.dequantize(got, to_tensor(s, "f32"), to_tensor(b, "f32"), 32, 2,
+                            dtype=torch.float32)
+        q1 = O.unpack_rows(w, 1).astype(np.float32)
+        ref = (q1 * np.repeat(s, 32, axis=1)).astype(np.float32) + np.repeat(b, 32, axis=1)
+        np.testing.assert_array_equal(values_of(deq), ref)
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("shape,bs", [((5, 100), 64), ((4, 256), 128), ((3, 33), 32)])
+def test_dequantize_tensor_v1_flat(bits, shape, bs):
+    """Flat v1 stream (quantize.py:292-326), f16 sidecars, padded last block: bit-exact."""
+    rng = np.random.default_rng(bits * 7 + bs)
+    total = int(np.prod(shape))
+    n_blocks = -(-total // bs)
+    q = O.pack_bits(rng.integers(0, 1 << bits, size=n_blocks * bs), bits)
+    s = (rng.random(n_blocks) * 0.1 + 1e-3).astype(np.float16)
+    b = (rng.standard_normal(n_blocks) * 0.05).astype(np.float16)
+    got = jq.dequantize_tensor(torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(),
+                               torch.from_numpy(b).cuda(), bits, shape, bs)
+    assert got.dtype == torch.float32 and tuple(got.shape) == shape
+    np.testing.assert_array_equal(values_of(got), O.dequantize_tensor_flat(q, s, b, bits, shape, bs))

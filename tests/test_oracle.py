@@ -366,3 +366,43 @@ def test_swiglu_pair_equals_switch_glu_single_expert():
     stack = [(m[0][None], m[1][None], m[2][None], m[3]) for m in mats]
     _, hs = O.switch_glu(x, np.zeros((T, 1), np.int64), *stack, 64, "bf16")
     np.testing.assert_array_equal(h, hs[:, 0, :])
+
+
+def test_expand_1bit_to_2bit_known_answers_and_codes():
+    """Known answers from the definition (source bit i -> 2-bit field i, low half of a word
+    to the even output word, high half to the odd one) and the code-level identity."""
+    src = np.array([[0x80000001, 0xFFFFFFFF, 0x0000FFFF, 0x00010000]], np.uint32)
+    got = O.expand_1bit_to_2bit(src)
+    assert got.tolist() == [[0x00000001, 0x40000000, 0x55555555, 0x55555555,
+                             0x55555555, 0x00000000, 0x00000000, 0x00000001]]
+    rng = np.random.default_rng(3)
+    w = rng.integers(0, 2**32, size=(7, 5), dtype=np.uint64).astype(np.uint32)
+    e = O.expand_1bit_to_2bit(w)
+    assert e.shape == (7, 10)
+    np.testing.assert_array_equal(O.unpack_rows(e, 2), O.unpack_rows(w, 1))
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+def test_dequantize_tensor_flat_vs_loop_and_row_layout(bits):
+    """quantize.py:292-326 on a padded tensor: a per-element loop over the bit stream, and the
+    same bytes read as the row layout of [n_blocks, 64] (the identity the GPU path uses)."""
+    rng = np.random.default_rng(bits)
+    shape, bs = (3, 50), 64
+    n_blocks = -(-150 // bs)
+    codes = rng.integers(0, 1 << bits, size=n_blocks * bs)
+    q = O.pack_bits(codes, bits)
+    s = (rng.random(n_blocks) * 0.1 + 0.01).astype(np.float16)
+    b = (rng.standard_normal(n_blocks) * 0.05).astype(np.float16)
+    got = O.dequantize_tensor_flat(q, s, b, bits, shape, bs)
+    loop = np.empty(150, np.float32)
+    for i in range(150):
+        v = 0
+        for t in range(bits):
+            bit = i * bits + t
+            v |= ((int(q[bit // 8]) >> (bit % 8)) & 1) << t
+        blk = i // bs
+        loop[i] = np.float32(np.float32(v) * np.float32(s[blk])) + np.float32(b[blk])
+    np.testing.assert_array_equal(got.reshape(-1), loop)
+    rows = O.dequantize_affine(q.view(np.uint32).reshape(n_blocks, bs * bits // 32),
+                               s.astype(np.float32)[:, None], b.astype(np.float32)[:, None], bits, bs)
+    np.testing.assert_array_equal(got.reshape(-1), rows.reshape(-1)[:150])
