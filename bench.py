@@ -266,9 +266,11 @@ def bench_moe(gen, name, E, H, I, bits, gs, k, T, steps, warmup, shared_I=None, 
 # ----------------------------------------------------------------------------- CPU baseline
 
 
-def cpu_baseline_c2(max_seconds=30.0):
+def cpu_baseline_c2(min_seconds=10.0, max_seconds=30.0):
     """The reference CPU path restated (oracle/): numpy dequant (affine.py:445-463) then
-    BLAS fp32 x @ W^T, for the config-2 block at batch 1, on this host's cores."""
+    BLAS fp32 x @ W^T, for the config-2 block at batch 1, on this host's cores. The block's
+    seven projections are quantized once and then run in passes until at least min_seconds of
+    timed CPU work (bounded by max_seconds)."""
     import numpy as np
 
     cores = len(os.sched_getaffinity(0))
@@ -278,29 +280,35 @@ def cpu_baseline_c2(max_seconds=30.0):
     H, I = 4096, 14336
     shapes = [((4096, H), 6), ((1024, H), 6), ((1024, H), 6), ((H, 4096), 6), ((I, H), 3),
               ((I, H), 3), ((H, I), 2)]
-    t_deq = t_mm = 0.0
-    nbytes = 0
-    done = 0
+    mats = []
     for (N, K), bits in shapes:
         w = O.round_bf16(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
         packed, s, b, _ = O.quantize_affine(w, bits, 64)
-        sf, bf = O.sidecar_f32(s, "bf16"), O.sidecar_f32(b, "bf16")
         x = O.round_bf16(rng.standard_normal((1, K), dtype=np.float32))
-        t0 = time.perf_counter()
-        W = O.dequantize_affine(packed, sf, bf, bits, 64)
-        t1 = time.perf_counter()
-        y = x @ W.T
-        t2 = time.perf_counter()
-        t_deq += t1 - t0
-        t_mm += t2 - t1
-        nbytes += N * K * bits // 8 + N * (K // 64) * 4 + 2 * K + 2 * N
-        done += 1
+        mats.append((packed, O.sidecar_f32(s, "bf16"), O.sidecar_f32(b, "bf16"), bits, x, N, K))
+    t_deq = t_mm = 0.0
+    nbytes = 0
+    done = 0
+    while t_deq + t_mm < min_seconds:
+        for packed, sf, bf, bits, x, N, K in mats:
+            t0 = time.perf_counter()
+            W = O.dequantize_affine(packed, sf, bf, bits, 64)
+            t1 = time.perf_counter()
+            y = x @ W.T
+            t2 = time.perf_counter()
+            t_deq += t1 - t0
+            t_mm += t2 - t1
+            nbytes += N * K * bits // 8 + N * (K // 64) * 4 + 2 * K + 2 * N
+            done += 1
+            if t_deq + t_mm > max_seconds:
+                break
         if t_deq + t_mm > max_seconds:
             break
     secs = t_deq + t_mm
     return {"value": round(nbytes / secs / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"{done}/7 projections of the config-2 block at batch 1: numpy dequant "
-                      f"({t_deq:.2f} s) + BLAS fp32 matmul ({t_mm:.2f} s), vectorised unpack",
+            "sample": f"{done} projections ({done / 7:.1f} passes over the config-2 block at batch "
+                      f"1): numpy dequant ({t_deq:.2f} s) + BLAS fp32 matmul ({t_mm:.2f} s), "
+                      f"vectorised unpack",
             "dequant_s": round(t_deq, 3), "matmul_s": round(t_mm, 3)}
 
 
