@@ -36,6 +36,7 @@ EXTRA = {
     "jq_dec.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "jq_decp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "jq_qmv4.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "jq_dmx.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

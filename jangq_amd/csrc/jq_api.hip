@@ -1,7 +1,8 @@
 // Dense matmul entry points: dispatch between the vector-ALU decode GEMV (M <= 4), the
 // decode-batch matrix-core kernels (up to 64 rows: 4x4x4 blocks for long rows, the
-// persistent 16x16x32 kernel otherwise), the prefill GEMM and, for shapes none of those
-// takes, the older LDS-tiled GEMM or the generic GEMV.
+// LDS-streamed 16x16x32 kernel for K <= 4096, the register-streamed one otherwise), the
+// prefill GEMM and, for shapes none of those takes, the older LDS-tiled GEMM or the generic
+// GEMV.
 #include "jq_common.h"
 #include "jq_qmv.h"
 
@@ -39,6 +40,14 @@ int dense_one(const void* x, int xd, const uint32_t* codes, const void* scales,
     b.p[0].x = x; b.p[0].codes = codes; b.p[0].scales = scales; b.p[0].biases = biases;
     b.p[0].y = y; b.p[0].N = N;
     return jqk::qmv4_launch(b, 1, bits, gs, xd, sb, yd, st);
+  }
+  if (M <= kDecpMaxRows && jqk::dmx_ok(Mi, K, N, bits, gs, xd, sb, 1)) {
+    jqk::QmvBatch b;
+    b.M = Mi;
+    b.K = (int)K;
+    b.p[0].x = x; b.p[0].codes = codes; b.p[0].scales = scales; b.p[0].biases = biases;
+    b.p[0].y = y; b.p[0].N = N;
+    return jqk::dmx_launch(b, 1, bits, gs, xd, sb, yd, st);
   }
   if (M <= kDecpMaxRows && jqk::decp_ok(Mi, K, N, xd, sb)) {
     jqk::QmvBatch b;
@@ -148,8 +157,10 @@ int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
   const bool gemv = same && jqk::gemv_ok(M0, K[0], maxN, bits[0], group_size[0], x_dtype, sb_dtype);
   const bool q4 = same && !gemv && use_qmv4(M[0], K[0]) &&
                   jqk::qmv4_ok(M0, K[0], maxN, bits[0], group_size[0], x_dtype, sb_dtype);
+  const bool dmx = same && !gemv && !q4 && M[0] <= kDecpMaxRows &&
+                   jqk::dmx_ok(M0, K[0], maxN, bits[0], group_size[0], x_dtype, sb_dtype, 1);
   const bool dec = same && M[0] <= kDecpMaxRows && jqk::decp_ok(M0, K[0], maxN, x_dtype, sb_dtype);
-  if (q4 || gemv || dec || (same && M[0] >= 1 && M[0] <= 4 && K[0] > 0)) {
+  if (q4 || gemv || dmx || dec || (same && M[0] >= 1 && M[0] <= 4 && K[0] > 0)) {
     jqk::QmvBatch b;
     b.M = (int)M[0];
     b.K = (int)K[0];
@@ -166,6 +177,7 @@ int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
     }
     if (gemv) return jqk::gemv_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
     if (q4) return jqk::qmv4_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
+    if (dmx) return jqk::dmx_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
     if (dec) return jqk::decp_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
     return jqk::qmv_launch(b, n, bits[0], group_size[0], x_dtype, sb_dtype, y_dtype, st);
   }

@@ -1,0 +1,738 @@
+// Decode-batch quantized matmul on matrix cores with the weights streamed through LDS by
+// direct-to-LDS buffer loads: y = x @ deq(W)^T for up to 2 * 16/(128/gs) activation rows per
+// pass, dense (one or several problems sharing x) or expert-gathered (MoE tiles of a plan).
+//
+// Arithmetic (jq_dec.h, as the register-streamed decode kernel): lane (r = l%16, g = l/16)
+// feeds unit g of each 128-code step of W row r into v_mfma_f32_16x16x32 B fragments; the
+// step's 128/gs groups are folded into the MFMA M dimension, so every accumulator slot
+// belongs to one (token, group) and takes  acc += s_g * D + b_g * X,  D = sum q*x exactly
+// (the per-group affine sum s * sum q x + b * sum x, jang-tools/jang_tools/dsv41/metal_decode.py:202-233).
+//
+// Memory path. Wave w of a block owns SW consecutive 128-code steps of every item (RT tiles
+// of 16 W rows). Per item it copies its piece of each row (SW*16*BITS bytes, contiguous in
+// HBM) and of the rows' scales and biases straight into its own LDS ring with
+// buffer_load ... lds: one instruction moves 1 KB as 8 rows x 128 B runs (16 B per lane), so
+// address and cache-line work per byte is that of a contiguous stream, where register
+// fragments would make every load instruction touch 16 rows. Rows sit at a stride of piece +
+// 16 B in LDS, which spreads the 16 rows of a fragment read over the banks. The ring holds
+// NSLOT items; the copy of item k + NSLOT - 1 is issued before item k is computed, and the
+// wave waits only for its own copies of item k (a vector-memory count, no barrier), so
+// NSLOT - 1 items of HBM traffic stay in flight. The activations of the wave's steps are
+// held in registers as A fragments (loaded once per pass, or per tile when gathering), with
+// their MFMA row sums X and offset sums O.
+//
+// One barrier per item: each wave writes its folded partials to LDS, then the waves sum the
+// KW partials, one output slot per wave in turn, and store them (gathered gate|up pairs:
+// h = silu(g) * u with the bf16 roundings of the stock path).
+#include "jq_gemv.h"
+#include "jq_qmv.h"
+
+#define JQ_LDS __attribute__((address_space(3)))
+
+namespace {
+
+using namespace jq;
+using namespace jqd;
+using jqg::Rsrc;
+using jqg::make_rsrc;
+using jqk::GatherPlan;
+using jqk::QmmProblem;
+using jqk::QmvBatch;
+using jqk::QmvProblem;
+
+constexpr int kMaxKW = 8;
+constexpr int kLdsMax = 150 * 1024;
+
+struct DmxArgs {
+  // dense
+  QmvBatch b;
+  int rb_begin[jqk::kMaxProblems + 1];
+  int nprob;
+  int m0, mrows;
+  // gathered
+  QmmProblem g[2];
+  GatherPlan plan;
+  // both
+  int nrb;     // gathered: row blocks per tile
+  int items;   // dense: total items (gathered: read from the plan)
+  int K;
+  int yd;
+};
+
+// Compile-time layout of one wave's ring.
+template <class D, int RT, int SW, int NSLOT>
+struct Ring {
+  static constexpr int PB = SW * 16 * D::BITS;                  // piece bytes per row
+  static constexpr int RS = PB + 16;                            // LDS row stride
+  static constexpr int CODE_INSTR = (16 * RS + 1023) / 1024;    // b128 copies per tile
+  static constexpr int CODE_AREA = CODE_INSTR * 1024;
+  static constexpr int SBP = SW * D::GSTEP * 2;                 // scale bytes per row piece
+  static constexpr int SB_INSTR = (16 * SBP + 255) / 256;       // b32 copies per tile and array
+  static constexpr int SB_AREA = SB_INSTR * 256;
+  static constexpr int TILE = CODE_AREA + 2 * SB_AREA;
+  static constexpr int SLOT = RT * TILE;
+  static constexpr int WAVE = NSLOT * SLOT;
+  static constexpr int ND = RT * (CODE_INSTR + 2 * SB_INSTR);   // copies per item and wave
+};
+
+// Wave-uniform reads of plan data through the constant address space: scalar loads, counted
+// by the LDS/scalar counter, so they never wait for the ring's copies.
+template <class T>
+JQ_DEV T ldc(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
+JQ_DEV float round_to(float v, int yd) {
+  if (yd == JQ_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  if (yd == JQ_F16) return f16_bits_to_f32(f32_to_f16_bits(v));
+  return v;
+}
+
+JQ_DEV void store_out(void* y, int64_t idx, float v, int yd) {
+  if (yd == JQ_BF16) ((uint16_t*)y)[idx] = f32_to_bf16_bits(v);
+  else if (yd == JQ_F16) ((uint16_t*)y)[idx] = f32_to_f16_bits(v);
+  else ((float*)y)[idx] = v;
+}
+
+// s_waitcnt with only the vector-memory count set (expcnt and lgkmcnt left free).
+template <int N>
+JQ_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier after this wave's LDS writes have landed. No memory fence: the fence of
+// __syncthreads would also wait for every outstanding copy into the ring.
+JQ_DEV void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// An item's source rows: per tile, a buffer view of its 16 code rows and of the scale and
+// bias rows (rows past the matrix, dead items and empty tiles are views of 0 bytes).
+template <int RT>
+struct ItemSrc {
+  Rsrc c[RT], s[RT], b[RT];
+};
+
+// Tile rows of a gathered item (wave-uniform): x row and output row of each token slot.
+template <int MP>
+struct Toks {
+  int64_t xrow[MP];
+  int64_t orow[MP];
+  bool live[MP];
+  int n;
+};
+
+template <int MP>
+JQ_DEV void tile_toks(const GatherPlan& pl, int4 tl, Toks<MP>& tk) {
+  tk.n = tl.z;
+#pragma unroll
+  for (int m = 0; m < MP; ++m) {
+    const int rr = tl.y + (m < tl.z ? m : 0);
+    const int Mp = pl.M;
+    const int pi = Mp == 1 ? rr : rr / Mp, mi = Mp == 1 ? 0 : rr - pi * Mp;
+    const uint32_t pair = ldc(pl.order + tl.w + pi);
+    const int64_t xr = (int64_t)(pl.lhs ? ldc(pl.lhs + pair) : pair / (uint32_t)pl.pair_div) * Mp + mi;
+    tk.live[m] = m < tl.z && xr < pl.x_rows;
+    tk.xrow[m] = tk.live[m] ? xr : 0;
+    tk.orow[m] = (int64_t)pair * Mp + mi;
+  }
+}
+
+// x row of token slot t (lane-varying t: a select chain, not an indexed register array).
+template <int MP>
+JQ_DEV bool tok_row(const Toks<MP>& tk, int t, int64_t& row) {
+  bool live = false;
+  row = 0;
+#pragma unroll
+  for (int q = 0; q < MP; ++q)
+    if (t == q) row = tk.xrow[q], live = tk.live[q];
+  return live;
+}
+
+template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB>
+struct Dmx {
+  using R = Ring<D, RT, SW, NSLOT>;
+  static constexpr int BITS = D::BITS, TPB = D::TPB, TPL = 4 / D::GSTEP;
+  static constexpr int MP = NA * TPB;            // token slots of a pass or tile
+  static constexpr int NOUT = RT * NA * TPL;     // partial outputs per lane per item
+  static constexpr bool PRE = NA * SW <= 4;      // X and O kept per step in registers
+
+  // Per-lane byte offsets of the copies inside a tile's rows (the same for every item):
+  // copy j, lane i lands at LDS byte 1024 j + 16 i of the tile = (row f / RS, byte f % RS);
+  // pad lanes and lanes past the 16 rows repeat row 0's first chunk.
+  struct Offs {
+    uint32_t c[R::CODE_INSTR];
+    uint32_t s[R::SB_INSTR];
+  };
+
+  static JQ_DEV void offsets(int lane, uint32_t rowbytes, uint32_t sbrow, int s0, Offs& o) {
+#pragma unroll
+    for (int j = 0; j < R::CODE_INSTR; ++j) {
+      const int f = 1024 * j + 16 * lane;
+      const int row = f / R::RS, byte = f % R::RS;
+      const bool ok = row < 16 && byte < R::PB;
+      o.c[j] = ok ? (uint32_t)row * rowbytes + (uint32_t)(s0 * 16 * BITS + byte)
+                  : (uint32_t)(s0 * 16 * BITS);
+    }
+#pragma unroll
+    for (int j = 0; j < R::SB_INSTR; ++j) {
+      const int f = 256 * j + 4 * lane;
+      const int row = f / R::SBP, byte = f % R::SBP;
+      const bool ok = row < 16;
+      o.s[j] = ok ? (uint32_t)row * sbrow + (uint32_t)(s0 * D::GSTEP * 2 + byte)
+                  : (uint32_t)(s0 * D::GSTEP * 2);
+    }
+  }
+
+  // Copy an item into a ring slot (always the same number of copies).
+  static JQ_DEV void copy(const ItemSrc<RT>& src, const Offs& o, JQ_LDS uint8_t* __restrict__ slot) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      JQ_LDS uint8_t* t = slot + r * R::TILE;
+#pragma unroll
+      for (int j = 0; j < R::CODE_INSTR; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(src.c[r], (JQ_LDS void*)(t + 1024 * j), 16, o.c[j], 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < R::SB_INSTR; ++j) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(src.s[r], (JQ_LDS void*)(t + R::CODE_AREA + 256 * j), 4, o.s[j], 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(src.b[r], (JQ_LDS void*)(t + R::CODE_AREA + R::SB_AREA + 256 * j), 4, o.s[j], 0, 0, 0);
+      }
+    }
+  }
+
+  // A fragments of the wave's steps for the token slots of a pass / tile, and their sums.
+  struct Act {
+    u32x4 A[NA][SW][4];
+    f32x4 X[PRE ? NA : 1][PRE ? SW : 1], O[PRE ? NA : 1][PRE ? SW : 1];
+  };
+
+  static JQ_DEV void sums(const u32x4 (&A)[4], f32x4& X, f32x4& O) {
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    const u32x4 ones = {D::ONE2, D::ONE2, D::ONE2, D::ONE2};
+    constexpr u32x4 BO0 = {bo_dword<D>(0, 0), bo_dword<D>(0, 1), bo_dword<D>(0, 2), bo_dword<D>(0, 3)};
+    constexpr u32x4 BO1 = {bo_dword<D>(1, 0), bo_dword<D>(1, 1), bo_dword<D>(1, 2), bo_dword<D>(1, 3)};
+    constexpr u32x4 BO2 = {bo_dword<D>(2, 0), bo_dword<D>(2, 1), bo_dword<D>(2, 2), bo_dword<D>(2, 3)};
+    constexpr u32x4 BO3 = {bo_dword<D>(3, 0), bo_dword<D>(3, 1), bo_dword<D>(3, 2), bo_dword<D>(3, 3)};
+    X = mfma16<D::XDT>(A[0], ones, zero);
+    X = mfma16<D::XDT>(A[1], ones, X);
+    X = mfma16<D::XDT>(A[2], ones, X);
+    X = mfma16<D::XDT>(A[3], ones, X);
+    O = mfma16<D::XDT>(A[0], BO0, zero);
+    O = mfma16<D::XDT>(A[1], BO1, O);
+    O = mfma16<D::XDT>(A[2], BO2, O);
+    O = mfma16<D::XDT>(A[3], BO3, O);
+  }
+
+  // Lane (lr, lg) of activation block ab feeds token slot ab*TPB + lr/GSTEP in the lane
+  // groups of group lr % GSTEP; other lanes read zeros.
+  template <class XRow>
+  static JQ_DEV void load_act(const uint16_t* x, int K, int s0, int lr, int lg, XRow xrow, Act& ac) {
+    const uint16_t* zero = (const uint16_t*)kZeroRow;
+#pragma unroll
+    for (int ab = 0; ab < NA; ++ab) {
+      const int t = ab * TPB + lr / D::GSTEP;
+      int64_t row;
+      const bool act = (lr % D::GSTEP) == lg / D::LPG && xrow(t, row);
+#pragma unroll
+      for (int d = 0; d < SW; ++d) {
+        XRaw r;
+        load_xraw(act ? x + row * K + (int64_t)(s0 + d) * 128 + 32 * lg : zero, r);
+        ac.A[ab][d][0] = a_frag<D, 0>(r);
+        ac.A[ab][d][1] = a_frag<D, 1>(r);
+        ac.A[ab][d][2] = a_frag<D, 2>(r);
+        ac.A[ab][d][3] = a_frag<D, 3>(r);
+      }
+    }
+    if constexpr (PRE) {
+#pragma unroll
+      for (int ab = 0; ab < NA; ++ab)
+#pragma unroll
+        for (int d = 0; d < SW; ++d) sums(ac.A[ab][d], ac.X[ab][d], ac.O[ab][d]);
+    }
+  }
+
+  // The MFMAs and scale terms of one item from its ring slot.
+  static JQ_DEV void compute(const JQ_LDS uint8_t* __restrict__ slot, const Act& ac, const Bases<D>& bs,
+                             int lr, int lg, f32x4 (&acc)[NA][RT]) {
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ab = 0; ab < NA; ++ab)
+#pragma unroll
+      for (int r = 0; r < RT; ++r) acc[ab][r] = zero;
+#pragma unroll
+    for (int d = 0; d < SW; ++d) {
+      f32x4 X[NA], O[NA];
+#pragma unroll
+      for (int ab = 0; ab < NA; ++ab) {
+        if constexpr (PRE) {
+          X[ab] = ac.X[ab][d];
+          O[ab] = ac.O[ab][d];
+        } else {
+          sums(ac.A[ab][d], X[ab], O[ab]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        const JQ_LDS uint8_t* t = slot + r * R::TILE;
+        uint32_t w[BITS];
+        const JQ_LDS uint32_t* cw = (const JQ_LDS uint32_t*)(t + lr * R::RS + (4 * d + lg) * 4 * BITS);
+#pragma unroll
+        for (int q = 0; q < BITS; ++q) w[q] = cw[q];
+        uint32_t sw[(D::GSTEP + 1) / 2], bw[(D::GSTEP + 1) / 2];
+        const int sbo = lr * R::SBP + d * D::GSTEP * 2;
+        if constexpr (D::GSTEP == 1) {
+          sw[0] = *(const JQ_LDS uint16_t*)(t + R::CODE_AREA + sbo);
+          bw[0] = *(const JQ_LDS uint16_t*)(t + R::CODE_AREA + R::SB_AREA + sbo);
+        } else {
+#pragma unroll
+          for (int q = 0; q < (D::GSTEP + 1) / 2; ++q) {
+            sw[q] = *(const JQ_LDS uint32_t*)(t + R::CODE_AREA + sbo + 4 * q);
+            bw[q] = *(const JQ_LDS uint32_t*)(t + R::CODE_AREA + R::SB_AREA + sbo + 4 * q);
+          }
+        }
+        f32x4 Dd[NA], Dh[NA];
+#pragma unroll
+        for (int ab = 0; ab < NA; ++ab) { Dd[ab] = O[ab]; Dh[ab] = zero; }
+#define JQ_F(F)                                                                  \
+        {                                                                        \
+          u32x4 B, BH;                                                           \
+          b_frag<D, F>(w, bs, B, BH);                                            \
+          _Pragma("unroll") for (int ab = 0; ab < NA; ++ab) {                    \
+            Dd[ab] = mfma16<D::XDT>(ac.A[ab][d][F], B, Dd[ab]);                  \
+            if constexpr (D::NIB) Dh[ab] = mfma16<D::XDT>(ac.A[ab][d][F], BH, Dh[ab]); \
+          }                                                                      \
+        }
+        JQ_F(0) JQ_F(1) JQ_F(2) JQ_F(3)
+#undef JQ_F
+        float sc[4], bi[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = i % D::GSTEP;
+          sc[i] = half_to_f32<SB>(sw[j >> 1], j & 1);
+          bi[i] = half_to_f32<SB>(bw[j >> 1], j & 1);
+        }
+#pragma unroll
+        for (int ab = 0; ab < NA; ++ab)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float dv = D::NIB ? fmaf(16.f, Dh[ab][i], Dd[ab][i]) : Dd[ab][i];
+            acc[ab][r][i] = fmaf(sc[i], dv, fmaf(bi[i], X[ab][i], acc[ab][r][i]));
+          }
+      }
+    }
+  }
+
+  // Item it: its tile (gathered) / problem (dense), first W row and source views.
+  static JQ_DEV void locate(const DmxArgs& a, int it, bool live, int& tile, int& p, int64_t& row0,
+                            int4& tl, ItemSrc<RT>& src) {
+    const uint32_t rowbytes = (uint32_t)(a.K / 32) * BITS * 4;
+    const uint32_t sbrow = (uint32_t)(a.K / D::GS) * 2;
+    if constexpr (GATHER) {
+      tile = it / a.nrb;
+      const int rb = it - tile * a.nrb;
+      if (live) {
+        const int* tp = (const int*)(a.plan.tiles + tile);
+        tl = make_int4(ldc(tp), ldc(tp + 1), ldc(tp + 2), ldc(tp + 3));
+      } else {
+        tl = make_int4(0, 0, 0, 0);
+      }
+      p = 0;
+      const int64_t N = a.g[0].N;
+      row0 = (int64_t)rb * (NB == 2 ? 16 : 16 * RT);
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        const QmmProblem& pb = a.g[NB == 2 ? r : 0];
+        const int64_t r0 = row0 + (NB == 2 ? 0 : 16 * r);
+        const int64_t left = N - r0;
+        const uint32_t rows = live && tl.z > 0 && left > 0 ? (uint32_t)(left < 16 ? left : 16) : 0u;
+        const int64_t e = tl.x;
+        src.c[r] = make_rsrc((const char*)(pb.codes + e * pb.expert_stride_codes) + r0 * rowbytes,
+                             rows * rowbytes);
+        const int64_t sb0 = e * pb.expert_stride_sb * 2 + r0 * sbrow;
+        src.s[r] = make_rsrc((const char*)pb.scales + sb0, rows * sbrow);
+        src.b[r] = make_rsrc((const char*)pb.biases + sb0, rows * sbrow);
+      }
+    } else {
+      tile = 0;
+      tl = make_int4(0, 0, 0, 0);
+      p = 0;
+#pragma unroll
+      for (int q = 1; q < jqk::kMaxProblems; ++q)
+        if (q < a.nprob && it >= a.rb_begin[q]) p = q;
+      const QmvProblem& pb = a.b.p[p];
+      row0 = (int64_t)(it - a.rb_begin[p]) * (16 * RT);
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        const int64_t r0 = row0 + 16 * r;
+        const int64_t left = pb.N - r0;
+        const uint32_t rows = live && left > 0 ? (uint32_t)(left < 16 ? left : 16) : 0u;
+        src.c[r] = make_rsrc((const char*)pb.codes + r0 * rowbytes, rows * rowbytes);
+        src.s[r] = make_rsrc((const char*)pb.scales + r0 * sbrow, rows * sbrow);
+        src.b[r] = make_rsrc((const char*)pb.biases + r0 * sbrow, rows * sbrow);
+      }
+    }
+  }
+
+  static JQ_DEV void run(const DmxArgs& a, JQ_LDS uint8_t* __restrict__ ring0,
+                         JQ_LDS uint8_t* __restrict__ ring1, JQ_LDS uint8_t* __restrict__ ring2,
+                         JQ_LDS float* __restrict__ red) {
+    const int items = GATHER ? ldc(a.plan.n_tiles) * a.nrb : a.items;
+    const int per = (items + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int first = blockIdx.x * per;
+    const int end = first + per < items ? first + per : items;
+    if (first >= end) return;  // whole block
+    const int KW = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
+    const int s0 = wave * SW;
+    const uint32_t rowbytes = (uint32_t)(a.K / 32) * BITS * 4;
+    const uint32_t sbrow = (uint32_t)(a.K / D::GS) * 2;
+    Offs o;
+    offsets(lane, rowbytes, sbrow, s0, o);
+
+    // Ring prologue: items first .. first + NSLOT - 2.
+    int tile, p;
+    int64_t row0;
+    int4 tl;
+    ItemSrc<RT> src;
+#pragma unroll
+    for (int k = 0; k < NSLOT - 1; ++k) {
+      const int it = first + k;
+      locate(a, it < end ? it : end - 1, it < end, tile, p, row0, tl, src);
+      copy(src, o, k == 0 ? ring0 : k == 1 ? ring1 : ring2);
+      asm volatile("" ::: "memory");
+    }
+    // The first item's own coordinates.
+    locate(a, first, true, tile, p, row0, tl, src);
+    Act ac;
+    Toks<GATHER ? MP : 1> tk;
+    if constexpr (GATHER) {
+      tile_toks<MP>(a.plan, tl, tk);
+      load_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg, [&](int t, int64_t& row) { return tok_row(tk, t, row); }, ac);
+    } else {
+      load_act((const uint16_t*)a.b.p[0].x, a.K, s0, lr, lg,
+               [&](int t, int64_t& row) { row = a.m0 + t; return t < a.mrows; }, ac);
+    }
+    const Bases<D> bs = make_bases<D>();
+
+    auto step = [&](int it, JQ_LDS uint8_t* __restrict__ cur, JQ_LDS uint8_t* __restrict__ fill) {
+      const int par = (it - first) & 1;  // partials double-buffered across consecutive items
+      // Copy of item it + NSLOT - 1 into the slot freed by item it - 1.
+      {
+        const int nx = it + NSLOT - 1;
+        int t2, p2;
+        int64_t r2;
+        int4 tl2;
+        ItemSrc<RT> s2;
+        locate(a, nx < end ? nx : end - 1, nx < end, t2, p2, r2, tl2, s2);
+        copy(s2, o, fill);
+      }
+      wait_vm<(NSLOT - 1) * R::ND < 63 ? (NSLOT - 1) * R::ND : 63>();
+      asm volatile("" ::: "memory");
+      f32x4 acc[NA][RT];
+      compute(cur, ac, bs, lr, lg, acc);
+      JQ_LDS float* mine = red + ((par * KW + wave) * NOUT) * 64;
+#pragma unroll
+      for (int ab = 0; ab < NA; ++ab)
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+          float v[TPL];
+          fold_groups<D>(acc[ab][r], v);
+#pragma unroll
+          for (int k = 0; k < TPL; ++k) mine[((ab * RT + r) * TPL + k) * 64 + lane] = v[k];
+        }
+      lds_barrier();
+      // Sum the waves' partials and store: output slot o = (ab, r, k); gathered gate|up
+      // pairs take r = 0 (gate) and r = 1 (up) together.
+      constexpr int NO = NB == 2 ? NOUT / 2 : NOUT;
+      for (int oi = wave; oi < NO; oi += KW) {
+        const int k = oi % TPL;
+        const int rr = NB == 2 ? 0 : (oi / TPL) % RT;
+        const int ab = NB == 2 ? oi / TPL : oi / (TPL * RT);
+        const int slot0 = (ab * RT + rr) * TPL + k;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < kMaxKW; ++w)
+          if (w < KW) v += red[((par * KW + w) * NOUT + slot0) * 64 + lane];
+        const int tok = ab * TPB + TPL * lg + k;
+        if constexpr (GATHER) {
+          const int64_t N = a.g[0].N;
+          const int64_t n = row0 + (NB == 2 ? 0 : 16 * rr) + lr;
+          if constexpr (NB == 2) {
+            float u = 0.f;
+            const int slot1 = (ab * RT + 1) * TPL + k;
+#pragma unroll
+            for (int w = 0; w < kMaxKW; ++w)
+              if (w < KW) u += red[((par * KW + w) * NOUT + slot1) * 64 + lane];
+            const float gg = round_to(v, a.yd), uu = round_to(u, a.yd);
+            v = gg / (1.0f + expf(-gg)) * uu;
+          }
+          int64_t orow = tk.orow[0];
+          bool live = 0 < tk.n;
+#pragma unroll
+          for (int q = 1; q < MP; ++q)
+            if (tok == q) orow = tk.orow[q], live = q < tk.n;
+          if (tok < MP && live && n < N) store_out(a.g[0].y, orow * N + n, v, a.yd);
+        } else {
+          const QmvProblem& pb = a.b.p[p];
+          const int64_t n = row0 + 16 * rr + lr;
+          if (tok < a.mrows && n < pb.N) store_out(pb.y, (int64_t)(a.m0 + tok) * pb.N + n, v, a.yd);
+        }
+      }
+      // Next item's coordinates (and, when its tile differs, its activations).
+      if (it + 1 < end) {
+        const int prev = tile;
+        locate(a, it + 1, true, tile, p, row0, tl, src);
+        if constexpr (GATHER) {
+          if (tile != prev) {
+            tile_toks<MP>(a.plan, tl, tk);
+            load_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg, [&](int t, int64_t& row) { return tok_row(tk, t, row); }, ac);
+          }
+        }
+      }
+    };
+
+    // Items in ring order (slot = k % NSLOT at compile time).
+    for (int it = first; it < end; it += NSLOT) {
+      step(it, ring0, NSLOT == 2 ? ring1 : ring2);
+      if (it + 1 >= end) break;
+      step(it + 1, ring1, ring0);
+      if constexpr (NSLOT == 3) {
+        if (it + 2 >= end) break;
+        step(it + 2, ring2, ring1);
+      }
+    }
+  }
+};
+
+template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB>
+__global__ void __launch_bounds__(64 * kMaxKW) dmx_kernel(DmxArgs a) {
+  using K = Dmx<D, SB, RT, NA, SW, NSLOT, GATHER, NB>;
+  using R = typename K::R;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t dmx_lds[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int KW = blockDim.x >> 6;
+  JQ_LDS uint8_t* base = (JQ_LDS uint8_t*)dmx_lds;
+  JQ_LDS uint8_t* w0 = base + wave * R::WAVE;
+  JQ_LDS float* red = (JQ_LDS float*)(base + KW * R::WAVE);
+  K::run(a, w0, w0 + R::SLOT, w0 + (NSLOT == 3 ? 2 : 1) * R::SLOT, red);
+}
+
+template <class D, int RT, int NA, int SW, int NSLOT>
+constexpr size_t dmx_lds_bytes(int kw) {
+  using R = Ring<D, RT, SW, NSLOT>;
+  return (size_t)kw * R::WAVE + (size_t)2 * kw * RT * NA * (4 / D::GSTEP) * 64 * 4;
+}
+
+template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB>
+int launch_cfg(DmxArgs& a, int kw, int64_t max_items, hipStream_t st) {
+  const size_t lds = dmx_lds_bytes<D, RT, NA, SW, NSLOT>(kw);
+  if (lds > (size_t)kLdsMax) return JQ_ERR_SHAPE;
+  auto kern = dmx_kernel<D, SB, RT, NA, SW, NSLOT, GATHER, NB>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
+    return JQ_ERR_LAUNCH;
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 64 * kw, lds) != hipSuccess || nb < 1)
+    nb = 1;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  const int64_t cap = (int64_t)nb * cus;
+  int64_t grid;
+  if constexpr (GATHER) {
+    grid = max_items < cap ? max_items : cap;  // items are read from the plan on the device
+  } else {
+    const int64_t iters = (max_items + cap - 1) / cap;
+    grid = (max_items + iters - 1) / iters;
+  }
+  if (grid < 1) return JQ_OK;
+  kern<<<(unsigned)grid, 64 * kw, lds, st>>>(a);
+  return jqh::launch_status();
+}
+
+// Ring depth: three items when they fit the LDS budget at kMaxKW waves, else two.
+template <class D, int RT, int NA, int SW>
+constexpr int ring_slots() {
+  return dmx_lds_bytes<D, RT, NA, SW, 3>(kMaxKW) <= (size_t)kLdsMax ? 3 : 2;
+}
+
+// Steps per wave: 4 when K has a multiple of 4 steps that at most kMaxKW waves cover, else 2.
+inline int dmx_sw(int K) {
+  const int S = K / 128;
+  if (S % 4 == 0 && S / 4 <= kMaxKW) return 4;
+  if (S % 2 == 0 && S / 2 <= kMaxKW) return 2;
+  return 0;
+}
+
+template <class D, int SB, int RT, int NA, bool GATHER, int NB>
+int launch_sw(DmxArgs& a, int64_t max_items, hipStream_t st) {
+  const int sw = dmx_sw(a.K);
+  const int kw = sw ? a.K / 128 / sw : 0;
+  if (sw == 2)
+    return launch_cfg<D, SB, RT, NA, 2, ring_slots<D, RT, NA, 2>(), GATHER, NB>(a, kw, max_items, st);
+  if (sw == 4)
+    return launch_cfg<D, SB, RT, NA, 4, ring_slots<D, RT, NA, 4>(), GATHER, NB>(a, kw, max_items, st);
+  return JQ_ERR_SHAPE;
+}
+
+// Dense: passes of TPB (one activation block) or 2 TPB rows.
+template <int BITS, int GS, int XDT, int SB>
+int dense_t(const QmvBatch& b, int nprob, int yd, hipStream_t st) {
+  using D = Dc<BITS, GS, XDT>;
+  const int pass = b.M > D::TPB ? 2 * D::TPB : D::TPB;
+  for (int m0 = 0; m0 < b.M; m0 += pass) {
+    DmxArgs a;
+    a.b = b;
+    a.nprob = nprob;
+    a.m0 = m0;
+    a.mrows = b.M - m0 < pass ? b.M - m0 : pass;
+    a.K = b.K;
+    a.yd = yd;
+    a.nrb = 0;
+    int s;
+    constexpr int RT = 1;
+    int total = 0;
+    for (int i = 0; i < nprob; ++i) {
+      a.rb_begin[i] = total;
+      total += (int)((b.p[i].N + 16 * RT - 1) / (16 * RT));
+    }
+    for (int i = nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
+    a.items = total;
+    if (total == 0) return JQ_OK;
+    if (pass > D::TPB) s = launch_sw<D, SB, RT, 2, false, 1>(a, total, st);
+    else s = launch_sw<D, SB, RT, 1, false, 1>(a, total, st);
+    if (s) return s;
+  }
+  return JQ_OK;
+}
+
+template <int XDT, int SB>
+int dense_bits(int bits, int gs, const QmvBatch& b, int nprob, int yd, hipStream_t st) {
+#define JQ_D(B)                                                    \
+  switch (gs) {                                                    \
+    case 64: return dense_t<B, 64, XDT, SB>(b, nprob, yd, st);     \
+    default: return dense_t<B, 128, XDT, SB>(b, nprob, yd, st);    \
+  }
+  switch (bits) {
+    case 2: JQ_D(2)
+    case 3: JQ_D(3)
+    case 4: JQ_D(4)
+    case 5: JQ_D(5)
+    case 6: JQ_D(6)
+    default: JQ_D(8)
+  }
+#undef JQ_D
+}
+
+// Gathered: tiles of up to TPB token rows (one activation block).
+template <int BITS, int GS, int XDT, int SB, int NB>
+int gather_t(DmxArgs& a, int64_t max_tiles, hipStream_t st) {
+  using D = Dc<BITS, GS, XDT>;
+  constexpr int RT = NB;
+  const int64_t N = a.g[0].N;
+  a.nrb = (int)((N + (NB == 2 ? 16 : 16 * RT) - 1) / (NB == 2 ? 16 : 16 * RT));
+  const int64_t max_items = max_tiles * a.nrb;
+  if (max_items == 0) return JQ_OK;
+  if (max_items >= ((int64_t)1 << 31)) return JQ_ERR_SHAPE;
+  return launch_sw<D, SB, RT, 1, true, NB>(a, max_items, st);
+}
+
+template <int XDT, int SB, int NB>
+int gather_bits(int bits, int gs, DmxArgs& a, int64_t max_tiles, hipStream_t st) {
+#define JQ_G(B)                                                         \
+  switch (gs) {                                                         \
+    case 64: return gather_t<B, 64, XDT, SB, NB>(a, max_tiles, st);     \
+    default: return gather_t<B, 128, XDT, SB, NB>(a, max_tiles, st);    \
+  }
+  switch (bits) {
+    case 2: JQ_G(2)
+    case 3: JQ_G(3)
+    case 4: JQ_G(4)
+    case 5: JQ_G(5)
+    case 6: JQ_G(6)
+    default: JQ_G(8)
+  }
+#undef JQ_G
+}
+
+}  // namespace
+
+namespace jqk {
+
+// LDS bytes of the smallest ring (two items) of one block, as Ring lays it out.
+size_t dmx_min_lds(int bits, int gs, int K, int rt, int na) {
+  const int sw = dmx_sw(K), kw = K / 128 / sw, gstep = 128 / gs;
+  const int pb = sw * 16 * bits, rs = pb + 16;
+  const int code = (16 * rs + 1023) / 1024 * 1024;
+  const int sbp = sw * gstep * 2;
+  const int sbarea = (16 * sbp + 255) / 256 * 256;
+  const size_t wave = (size_t)2 * rt * (code + 2 * sbarea);
+  return (size_t)kw * wave + (size_t)2 * kw * rt * na * (4 / gstep) * 64 * 4;
+}
+
+bool dmx_ok(int M, int64_t K, int64_t maxN, int bits, int gs, int xd, int sb, int rt) {
+  if ((xd != JQ_BF16 && xd != JQ_F16) || sb != xd) return false;
+  if (gs != 64 && gs != 128) return false;
+  if (bits < 2 || bits > 8 || bits == 7) return false;
+  if (K <= 0 || K % 128 || K > 4 * kMaxKW * 128 || dmx_sw((int)K) == 0) return false;
+  const int tpb = 16 / (128 / gs);
+  if (M < 1 || maxN >= ((int64_t)1 << 30)) return false;  // passes of up to 2 * tpb rows
+  return dmx_min_lds(bits, gs, (int)K, rt, M > tpb ? 2 : 1) <= (size_t)kLdsMax;
+}
+
+int dmx_tokens_per_tile(int gs) { return 16 / (128 / gs); }
+
+int dmx_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
+               hipStream_t st) {
+  int64_t maxN = 0;
+  for (int i = 0; i < nprob; ++i) maxN = b.p[i].N > maxN ? b.p[i].N : maxN;
+  if (maxN == 0 || b.M == 0) return JQ_OK;
+  if (!dmx_ok(b.M, b.K, maxN, bits, gs, xd, sb, 1)) return JQ_ERR_SHAPE;
+  for (int i = 1; i < nprob; ++i) {
+    if (b.p[i].x != b.p[0].x) {  // the activations are those of problem 0
+      for (int j = 0; j < nprob; ++j) {
+        QmvBatch one = b;
+        one.p[0] = b.p[j];
+        const int s = dmx_launch(one, 1, bits, gs, xd, sb, yd, st);
+        if (s) return s;
+      }
+      return JQ_OK;
+    }
+  }
+  if (xd == JQ_BF16) return dense_bits<JQ_BF16, JQ_BF16>(bits, gs, b, nprob, yd, st);
+  return dense_bits<JQ_F16, JQ_F16>(bits, gs, b, nprob, yd, st);
+}
+
+bool dmx_gather_ok(int64_t N, int64_t K, int bits, int gs, int xd, int sb, int nb) {
+  return dmx_ok(1, K, N, bits, gs, xd, sb, nb);
+}
+
+int dmx_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPlan& plan,
+                      int64_t max_tiles, int bits, int gs, int xd, int sb, int yd,
+                      hipStream_t st) {
+  if (max_tiles == 0 || p.N == 0) return JQ_OK;
+  if (!dmx_gather_ok(p.N, p.K, bits, gs, xd, sb, p2 ? 2 : 1) || plan.tiles == nullptr)
+    return JQ_ERR_SHAPE;
+  DmxArgs a;
+  a.g[0] = p;
+  a.g[1] = p2 ? *p2 : p;
+  a.plan = plan;
+  a.K = (int)p.K;
+  a.yd = yd;
+  a.nprob = 0;
+  a.items = 0;
+  if (xd == JQ_BF16)
+    return p2 ? gather_bits<JQ_BF16, JQ_BF16, 2>(bits, gs, a, max_tiles, st)
+              : gather_bits<JQ_BF16, JQ_BF16, 1>(bits, gs, a, max_tiles, st);
+  return p2 ? gather_bits<JQ_F16, JQ_F16, 2>(bits, gs, a, max_tiles, st)
+            : gather_bits<JQ_F16, JQ_F16, 1>(bits, gs, a, max_tiles, st);
+}
+
+}  // namespace jqk

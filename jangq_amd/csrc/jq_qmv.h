@@ -70,6 +70,20 @@ struct QmmProblem {
   int64_t expert_stride_sb;     // elements between experts' scale rows (gather mode)
 };
 
+// Decode batches on matrix cores with LDS-streamed weights (jq_dmx.hip): M <= 2*16/(128/gs),
+// gs 64/128, scales of the activation dtype, K % 256 == 0 and K <= 4096 (or K = 1024..2048
+// in 2-step waves), the ring within the LDS budget (rt: 16-row tiles per item).
+bool dmx_ok(int M, int64_t K, int64_t maxN, int bits, int gs, int xd, int sb, int rt);
+int dmx_tokens_per_tile(int gs);
+int dmx_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
+               hipStream_t st);
+// Expert-gathered form: plan tiles (plan.tiles != NULL) of up to dmx_tokens_per_tile rows;
+// with p2, gate (p) and up (p2) rows of each tile give h = silu(g) * u.
+bool dmx_gather_ok(int64_t N, int64_t K, int bits, int gs, int xd, int sb, int nb);
+int dmx_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPlan& plan,
+                      int64_t max_tiles, int bits, int gs, int xd, int sb, int yd,
+                      hipStream_t st);
+
 // Matrix-core GEMM y = x @ deq(W)^T. K % 128 == 0 required. Returns a jq_status.
 int qmm_launch(const QmmProblem& p, int bits, int gs, int xd, int sb, int yd, hipStream_t st);
 int gemm_launch(const QmmProblem& p, int bits, int gs, int xd, int sb, int yd, hipStream_t st);

@@ -89,6 +89,51 @@ def test_gather_qmm_mlx_broadcasting_and_sorted_flag():
     assert torch.equal(ys[torch.from_numpy(inv).cuda()].reshape(T, k, 1, N), y)
 
 
+@pytest.mark.parametrize("bits,gs,M,xdt", [(2, 64, 1, "bf16"), (3, 128, 1, "bf16"),
+                                           (4, 128, 2, "bf16"), (6, 64, 1, "f16"),
+                                           (8, 128, 1, "bf16"), (5, 64, 1, "bf16")])
+def test_gather_qmm_matrix_core_tiles(bits, gs, M, xdt):
+    """Hundreds of plan rows over 16 experts (about 12 per expert, one skewed): the
+    matrix-core tiles with LDS-streamed weights; ragged N, gathered x rows, M rows per pair."""
+    E, N, K, n, B = 16, 100, 512, 200, 40
+    qw = QWeight(N, K, bits, gs, seed=bits * 3 + gs, experts=E, sidecar=xdt)
+    rng = np.random.default_rng(bits + gs + M)
+    x = O.round_to(rng.standard_normal((B, M, K), dtype=np.float32), xdt)
+    lhs = rng.integers(0, B, size=n).astype(np.int32)
+    rhs = rng.integers(0, E, size=n).astype(np.int32)
+    rhs[:9] = 5
+    y = jq.gather_qmm(to_tensor(x, xdt), qw.dw, qw.ds, qw.db, torch.from_numpy(lhs).cuda(),
+                      torch.from_numpy(rhs).cuda(), group_size=gs, bits=bits)
+    ref = O.gather_qmm(x, qw.packed, qw.s, qw.b, lhs, rhs, bits, gs)
+    assert tuple(y.shape) == (n, M, N)
+    assert_close(values_of(y), O.round_to(ref, xdt), f"gather tiles b{bits} g{gs} M{M} {xdt}",
+                 exact=ref, out_dtype=xdt)
+
+
+@pytest.mark.parametrize("T,k,E,H,I,bits_gu,bits_d,gs,xdt",
+                         [(64, 4, 32, 512, 256, 2, 2, 64, "bf16"),
+                          (64, 4, 32, 512, 256, 3, 4, 64, "bf16"),
+                          (64, 4, 32, 512, 256, 2, 3, 128, "bf16"),
+                          (64, 4, 32, 512, 384, 4, 2, 64, "f16"),
+                          (32, 4, 16, 4096, 512, 2, 2, 64, "bf16")])
+def test_switch_glu_matrix_core_tiles(T, k, E, H, I, bits_gu, bits_d, gs, xdt):
+    """SwitchGLU with several tokens per selected expert: gate|up (+ SiLU) and down on the
+    matrix-core tiles (K = 4096 spreads a row over eight waves)."""
+    g = QWeight(I, H, bits_gu, gs, seed=31, experts=E, sidecar=xdt)
+    u = QWeight(I, H, bits_gu, gs, seed=32, experts=E, sidecar=xdt)
+    d = QWeight(H, I, bits_d, gs, seed=33, experts=E, sidecar=xdt)
+    rng = np.random.default_rng(T + H)
+    x = O.round_to(rng.standard_normal((T, H), dtype=np.float32), xdt)
+    inds = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    out = jq.switch_glu(to_tensor(x, xdt), torch.from_numpy(inds).cuda(),
+                        (g.dw, g.ds, g.db, bits_gu), (u.dw, u.ds, u.db, bits_gu),
+                        (d.dw, d.ds, d.db, bits_d), gs)
+    ref, _ = O.switch_glu(x, inds, (g.packed, g.s, g.b, bits_gu), (u.packed, u.s, u.b, bits_gu),
+                          (d.packed, d.s, d.b, bits_d), gs, xdt)
+    assert tuple(out.shape) == (T, k, H)
+    assert_close(values_of(out), ref, f"switch_glu tiles T{T} H{H} I{I} {xdt}")
+
+
 @pytest.mark.parametrize("T,k,E,bits_gu,bits_d", [(1, 4, 32, 2, 2), (16, 4, 32, 2, 2),
                                                   (64, 4, 32, 3, 4), (7, 2, 8, 8, 6),
                                                   (160, 2, 4, 2, 3)])
