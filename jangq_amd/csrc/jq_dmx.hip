@@ -41,7 +41,7 @@ using jqk::QmvBatch;
 using jqk::QmvProblem;
 
 constexpr int kMaxKW = 8;
-constexpr int kLdsMax = 150 * 1024;
+constexpr int kLdsMax = 156 * 1024;
 
 struct DmxArgs {
   // dense
@@ -64,15 +64,19 @@ template <class D, int RT, int SW, int NSLOT>
 struct Ring {
   static constexpr int PB = SW * 16 * D::BITS;                  // piece bytes per row
   static constexpr int RS = PB + 16;                            // LDS row stride
-  static constexpr int CODE_INSTR = (16 * RS + 1023) / 1024;    // b128 copies per tile
-  static constexpr int CODE_AREA = CODE_INSTR * 1024;
+  // A tile's rows fill 16 * RS bytes exactly: copies of 16 B per lane (1 KB each), then
+  // copies of 4 B per lane (256 B each) for the rest.
+  static constexpr int CODE_INSTR = 16 * RS / 1024;             // b128 copies per tile
+  static constexpr int TAIL_INSTR = (16 * RS - 1024 * CODE_INSTR) / 256;  // b32 copies
+  static constexpr int CODE_AREA = 16 * RS;
+  static_assert((16 * RS) % 256 == 0, "whole b32 copies");
   static constexpr int SBP = SW * D::GSTEP * 2;                 // scale bytes per row piece
   static constexpr int SB_INSTR = (16 * SBP + 255) / 256;       // b32 copies per tile and array
   static constexpr int SB_AREA = SB_INSTR * 256;
   static constexpr int TILE = CODE_AREA + 2 * SB_AREA;
   static constexpr int SLOT = RT * TILE;
   static constexpr int WAVE = NSLOT * SLOT;
-  static constexpr int ND = RT * (CODE_INSTR + 2 * SB_INSTR);   // copies per item and wave
+  static constexpr int ND = RT * (CODE_INSTR + TAIL_INSTR + 2 * SB_INSTR);  // copies per item
 };
 
 // Wave-uniform reads of plan data through the constant address space: scalar loads, counted
@@ -117,40 +121,37 @@ struct ItemSrc {
   Rsrc c[RT], s[RT], b[RT];
 };
 
-// Tile rows of a gathered item (wave-uniform): x row and output row of each token slot.
-template <int MP>
-struct Toks {
-  int64_t xrow[MP];
-  int64_t orow[MP];
-  bool live[MP];
-  int n;
+// Token rows of a gathered tile, per lane: the x row this lane's A fragments read (slot
+// xt = lr / GSTEP) and the output rows of the TPL token slots it stores (TPL * lg + k).
+template <int TPL>
+struct LaneToks {
+  int64_t xrow;
+  bool xlive;
+  int64_t orow[TPL];
+  bool olive[TPL];
 };
 
-template <int MP>
-JQ_DEV void tile_toks(const GatherPlan& pl, int4 tl, Toks<MP>& tk) {
-  tk.n = tl.z;
+template <int MP, int TPL>
+JQ_DEV void lane_toks(const GatherPlan& pl, int4 tl, int xt, int lg, LaneToks<TPL>& lt) {
+  lt.xrow = 0;
+  lt.xlive = false;
+#pragma unroll
+  for (int k = 0; k < TPL; ++k) lt.orow[k] = 0, lt.olive[k] = false;
 #pragma unroll
   for (int m = 0; m < MP; ++m) {
-    const int rr = tl.y + (m < tl.z ? m : 0);
-    const int Mp = pl.M;
-    const int pi = Mp == 1 ? rr : rr / Mp, mi = Mp == 1 ? 0 : rr - pi * Mp;
-    const uint32_t pair = ldc(pl.order + tl.w + pi);
-    const int64_t xr = (int64_t)(pl.lhs ? ldc(pl.lhs + pair) : pair / (uint32_t)pl.pair_div) * Mp + mi;
-    tk.live[m] = m < tl.z && xr < pl.x_rows;
-    tk.xrow[m] = tk.live[m] ? xr : 0;
-    tk.orow[m] = (int64_t)pair * Mp + mi;
-  }
-}
-
-// x row of token slot t (lane-varying t: a select chain, not an indexed register array).
-template <int MP>
-JQ_DEV bool tok_row(const Toks<MP>& tk, int t, int64_t& row) {
-  bool live = false;
-  row = 0;
+    if (m < tl.z) {  // wave-uniform
+      const int rr = tl.y + m;
+      const int Mp = pl.M;
+      const int pi = Mp == 1 ? rr : rr / Mp, mi = Mp == 1 ? 0 : rr - pi * Mp;
+      const uint32_t pair = ldc(pl.order + tl.w + pi);
+      const int64_t xr = (int64_t)(pl.lhs ? ldc(pl.lhs + pair) : pair / (uint32_t)pl.pair_div) * Mp + mi;
+      const bool live = xr < pl.x_rows;
+      if (xt == m) lt.xrow = live ? xr : 0, lt.xlive = live;
 #pragma unroll
-  for (int q = 0; q < MP; ++q)
-    if (t == q) row = tk.xrow[q], live = tk.live[q];
-  return live;
+      for (int k = 0; k < TPL; ++k)
+        if (TPL * lg + k == m) lt.orow[k] = (int64_t)pair * Mp + mi, lt.olive[k] = true;
+    }
+  }
 }
 
 template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB>
@@ -166,6 +167,7 @@ struct Dmx {
   // pad lanes and lanes past the 16 rows repeat row 0's first chunk.
   struct Offs {
     uint32_t c[R::CODE_INSTR];
+    uint32_t tail[R::TAIL_INSTR];  // the 4-byte copies of the rest
     uint32_t s[R::SB_INSTR];
   };
 
@@ -177,6 +179,14 @@ struct Dmx {
       const bool ok = row < 16 && byte < R::PB;
       o.c[j] = ok ? (uint32_t)row * rowbytes + (uint32_t)(s0 * 16 * BITS + byte)
                   : (uint32_t)(s0 * 16 * BITS);
+    }
+#pragma unroll
+    for (int j = 0; j < R::TAIL_INSTR; ++j) {
+      const int f = 1024 * R::CODE_INSTR + 256 * j + 4 * lane;
+      const int row = f / R::RS, byte = f % R::RS;
+      const bool ok = row < 16 && byte < R::PB;
+      o.tail[j] = ok ? (uint32_t)row * rowbytes + (uint32_t)(s0 * 16 * BITS + byte)
+                     : (uint32_t)(s0 * 16 * BITS);
     }
 #pragma unroll
     for (int j = 0; j < R::SB_INSTR; ++j) {
@@ -196,6 +206,9 @@ struct Dmx {
 #pragma unroll
       for (int j = 0; j < R::CODE_INSTR; ++j)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(src.c[r], (JQ_LDS void*)(t + 1024 * j), 16, o.c[j], 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < R::TAIL_INSTR; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(src.c[r], (JQ_LDS void*)(t + 1024 * R::CODE_INSTR + 256 * j), 4, o.tail[j], 0, 0, 0);
 #pragma unroll
       for (int j = 0; j < R::SB_INSTR; ++j) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(src.s[r], (JQ_LDS void*)(t + R::CODE_AREA + 256 * j), 4, o.s[j], 0, 0, 0);
@@ -379,7 +392,7 @@ struct Dmx {
 
   static JQ_DEV void run(const DmxArgs& a, JQ_LDS uint8_t* __restrict__ ring0,
                          JQ_LDS uint8_t* __restrict__ ring1, JQ_LDS uint8_t* __restrict__ ring2,
-                         JQ_LDS float* __restrict__ red) {
+                         JQ_LDS uint8_t* __restrict__ ring3, JQ_LDS float* __restrict__ red) {
     const int items = GATHER ? ldc(a.plan.n_tiles) * a.nrb : a.items;
     const int per = (items + (int)gridDim.x - 1) / (int)gridDim.x;
     const int first = blockIdx.x * per;
@@ -404,16 +417,16 @@ struct Dmx {
     for (int k = 0; k < NSLOT - 1; ++k) {
       const int it = first + k;
       locate(a, it < end ? it : end - 1, it < end, tile, p, row0, tl, src);
-      copy(src, o, k == 0 ? ring0 : k == 1 ? ring1 : ring2);
+      copy(src, o, k == 0 ? ring0 : k == 1 ? ring1 : ring2);  // k < NSLOT - 1 <= 3
       asm volatile("" ::: "memory");
     }
     // The first item's own coordinates.
     locate(a, first, true, tile, p, row0, tl, src);
     Act ac;
-    Toks<GATHER ? MP : 1> tk;
+    LaneToks<TPL> tk;
     if constexpr (GATHER) {
-      tile_toks<MP>(a.plan, tl, tk);
-      load_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg, [&](int t, int64_t& row) { return tok_row(tk, t, row); }, ac);
+      lane_toks<MP, TPL>(a.plan, tl, lr / D::GSTEP, lg, tk);
+      load_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg, [&](int, int64_t& row) { row = tk.xrow; return tk.xlive; }, ac);
     } else {
       load_act((const uint16_t*)a.b.p[0].x, a.K, s0, lr, lg,
                [&](int t, int64_t& row) { row = a.m0 + t; return t < a.mrows; }, ac);
@@ -432,7 +445,8 @@ struct Dmx {
         locate(a, nx < end ? nx : end - 1, nx < end, t2, p2, r2, tl2, s2);
         copy(s2, o, fill);
       }
-      wait_vm<(NSLOT - 1) * R::ND < 63 ? (NSLOT - 1) * R::ND : 63>();
+      static_assert((NSLOT - 1) * R::ND <= 63, "vmcnt range");
+      wait_vm<(NSLOT - 1) * R::ND>();
       asm volatile("" ::: "memory");
       f32x4 acc[NA][RT];
       compute(cur, ac, bs, lr, lg, acc);
@@ -473,11 +487,11 @@ struct Dmx {
             v = gg / (1.0f + expf(-gg)) * uu;
           }
           int64_t orow = tk.orow[0];
-          bool live = 0 < tk.n;
+          bool live = tk.olive[0];
 #pragma unroll
-          for (int q = 1; q < MP; ++q)
-            if (tok == q) orow = tk.orow[q], live = q < tk.n;
-          if (tok < MP && live && n < N) store_out(a.g[0].y, orow * N + n, v, a.yd);
+          for (int q = 1; q < TPL; ++q)
+            if (k == q) orow = tk.orow[q], live = tk.olive[q];
+          if (live && n < N) store_out(a.g[0].y, orow * N + n, v, a.yd);
         } else {
           const QmvProblem& pb = a.b.p[p];
           const int64_t n = row0 + 16 * rr + lr;
@@ -490,21 +504,34 @@ struct Dmx {
         locate(a, it + 1, true, tile, p, row0, tl, src);
         if constexpr (GATHER) {
           if (tile != prev) {
-            tile_toks<MP>(a.plan, tl, tk);
-            load_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg, [&](int t, int64_t& row) { return tok_row(tk, t, row); }, ac);
+            lane_toks<MP, TPL>(a.plan, tl, lr / D::GSTEP, lg, tk);
+            load_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg, [&](int, int64_t& row) { row = tk.xrow; return tk.xlive; }, ac);
           }
         }
       }
     };
 
-    // Items in ring order (slot = k % NSLOT at compile time).
+    // Items in ring order (slot = k % NSLOT at compile time): item k computes from slot
+    // k % NSLOT and refills slot (k - 1) % NSLOT.
     for (int it = first; it < end; it += NSLOT) {
-      step(it, ring0, NSLOT == 2 ? ring1 : ring2);
-      if (it + 1 >= end) break;
-      step(it + 1, ring1, ring0);
-      if constexpr (NSLOT == 3) {
+      if constexpr (NSLOT == 2) {
+        step(it, ring0, ring1);
+        if (it + 1 >= end) break;
+        step(it + 1, ring1, ring0);
+      } else if constexpr (NSLOT == 3) {
+        step(it, ring0, ring2);
+        if (it + 1 >= end) break;
+        step(it + 1, ring1, ring0);
         if (it + 2 >= end) break;
         step(it + 2, ring2, ring1);
+      } else {
+        step(it, ring0, ring3);
+        if (it + 1 >= end) break;
+        step(it + 1, ring1, ring0);
+        if (it + 2 >= end) break;
+        step(it + 2, ring2, ring1);
+        if (it + 3 >= end) break;
+        step(it + 3, ring3, ring2);
       }
     }
   }
@@ -520,7 +547,10 @@ __global__ void __launch_bounds__(64 * kMaxKW) dmx_kernel(DmxArgs a) {
   JQ_LDS uint8_t* base = (JQ_LDS uint8_t*)dmx_lds;
   JQ_LDS uint8_t* w0 = base + wave * R::WAVE;
   JQ_LDS float* red = (JQ_LDS float*)(base + KW * R::WAVE);
-  K::run(a, w0, w0 + R::SLOT, w0 + (NSLOT == 3 ? 2 : 1) * R::SLOT, red);
+  JQ_LDS uint8_t* s1 = w0 + R::SLOT;
+  JQ_LDS uint8_t* s2 = w0 + (NSLOT >= 3 ? 2 : 0) * R::SLOT;
+  JQ_LDS uint8_t* s3 = w0 + (NSLOT >= 4 ? 3 : 0) * R::SLOT;
+  K::run(a, w0, s1, s2, s3, red);
 }
 
 template <class D, int RT, int NA, int SW, int NSLOT>
@@ -557,10 +587,14 @@ int launch_cfg(DmxArgs& a, int kw, int64_t max_items, hipStream_t st) {
   return jqh::launch_status();
 }
 
-// Ring depth: three items when they fit the LDS budget at kMaxKW waves, else two.
+// Ring depth: the most items (4, 3 or 2) that fit the LDS budget at kMaxKW waves and the
+// vector-memory count.
 template <class D, int RT, int NA, int SW>
 constexpr int ring_slots() {
-  return dmx_lds_bytes<D, RT, NA, SW, 3>(kMaxKW) <= (size_t)kLdsMax ? 3 : 2;
+  constexpr int nd = Ring<D, RT, SW, 2>::ND;
+  if (dmx_lds_bytes<D, RT, NA, SW, 4>(kMaxKW) <= (size_t)kLdsMax && 3 * nd <= 63) return 4;
+  if (dmx_lds_bytes<D, RT, NA, SW, 3>(kMaxKW) <= (size_t)kLdsMax && 2 * nd <= 63) return 3;
+  return 2;
 }
 
 // Steps per wave: 4 when K has a multiple of 4 steps that at most kMaxKW waves cover, else 2.
@@ -670,7 +704,7 @@ namespace jqk {
 size_t dmx_min_lds(int bits, int gs, int K, int rt, int na) {
   const int sw = dmx_sw(K), kw = K / 128 / sw, gstep = 128 / gs;
   const int pb = sw * 16 * bits, rs = pb + 16;
-  const int code = (16 * rs + 1023) / 1024 * 1024;
+  const int code = 16 * rs;
   const int sbp = sw * gstep * 2;
   const int sbarea = (16 * sbp + 255) / 256 * 256;
   const size_t wave = (size_t)2 * rt * (code + 2 * sbarea);
