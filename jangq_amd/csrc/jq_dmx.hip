@@ -339,54 +339,97 @@ struct Dmx {
     }
   }
 
-  // Item it: its tile (gathered) / problem (dense), first W row and source views.
-  static JQ_DEV void locate(const DmxArgs& a, int it, bool live, int& tile, int& p, int64_t& row0,
-                            int4& tl, ItemSrc<RT>& src) {
-    const uint32_t rowbytes = (uint32_t)(a.K / 32) * BITS * 4;
-    const uint32_t sbrow = (uint32_t)(a.K / D::GS) * 2;
+  // Rows of W per item, and between the tiles of an item (gate|up pairs share their rows).
+  static constexpr int IROWS = NB == 2 ? 16 : 16 * RT;
+  static constexpr int TSTEP = NB == 2 ? 0 : 16;
+
+  // Wave-uniform walk over items in order: unit u (a plan tile when gathering, a problem
+  // otherwise) and row block rb inside it, with the unit's source base pointers. Moving to
+  // the next item needs no division; a new unit reloads its tile and bases.
+  struct Cursor {
+    int it, u, rb, nrb;
+    int64_t N;              // rows of the unit's matrices
+    int ez;                 // gathered: the tile has rows (0: nothing to read or store)
+    const char* cb[RT];     // codes of the unit's row 0 (per tile)
+    const char* sb[RT];     // scales
+    const char* bb[RT];     // biases
+  };
+
+  static JQ_DEV void unit_bases(const DmxArgs& a, Cursor& c, int4* tlo) {
     if constexpr (GATHER) {
-      tile = it / a.nrb;
-      const int rb = it - tile * a.nrb;
-      if (live) {
-        const int* tp = (const int*)(a.plan.tiles + tile);
+      int4 tl = make_int4(0, 0, 0, 0);
+      if (c.u < ldc(a.plan.n_tiles)) {
+        const int* tp = (const int*)(a.plan.tiles + c.u);
         tl = make_int4(ldc(tp), ldc(tp + 1), ldc(tp + 2), ldc(tp + 3));
-      } else {
-        tl = make_int4(0, 0, 0, 0);
       }
-      p = 0;
-      const int64_t N = a.g[0].N;
-      row0 = (int64_t)rb * (NB == 2 ? 16 : 16 * RT);
+      if (tlo) *tlo = tl;
+      c.ez = tl.z > 0;
+      c.N = a.g[0].N;
+      c.nrb = a.nrb;
 #pragma unroll
       for (int r = 0; r < RT; ++r) {
         const QmmProblem& pb = a.g[NB == 2 ? r : 0];
-        const int64_t r0 = row0 + (NB == 2 ? 0 : 16 * r);
-        const int64_t left = N - r0;
-        const uint32_t rows = live && tl.z > 0 && left > 0 ? (uint32_t)(left < 16 ? left : 16) : 0u;
         const int64_t e = tl.x;
-        src.c[r] = make_rsrc((const char*)(pb.codes + e * pb.expert_stride_codes) + r0 * rowbytes,
-                             rows * rowbytes);
-        const int64_t sb0 = e * pb.expert_stride_sb * 2 + r0 * sbrow;
-        src.s[r] = make_rsrc((const char*)pb.scales + sb0, rows * sbrow);
-        src.b[r] = make_rsrc((const char*)pb.biases + sb0, rows * sbrow);
+        c.cb[r] = (const char*)(pb.codes + e * pb.expert_stride_codes);
+        c.sb[r] = (const char*)pb.scales + e * pb.expert_stride_sb * 2;
+        c.bb[r] = (const char*)pb.biases + e * pb.expert_stride_sb * 2;
       }
     } else {
-      tile = 0;
-      tl = make_int4(0, 0, 0, 0);
-      p = 0;
-#pragma unroll
-      for (int q = 1; q < jqk::kMaxProblems; ++q)
-        if (q < a.nprob && it >= a.rb_begin[q]) p = q;
-      const QmvProblem& pb = a.b.p[p];
-      row0 = (int64_t)(it - a.rb_begin[p]) * (16 * RT);
+      if (tlo) *tlo = make_int4(0, 0, 0, 0);
+      const int u = c.u < a.nprob ? c.u : a.nprob - 1;
+      const QmvProblem& pb = a.b.p[u];
+      c.ez = 1;
+      c.N = pb.N;
+      c.nrb = a.rb_begin[u + 1] - a.rb_begin[u];
 #pragma unroll
       for (int r = 0; r < RT; ++r) {
-        const int64_t r0 = row0 + 16 * r;
-        const int64_t left = pb.N - r0;
-        const uint32_t rows = live && left > 0 ? (uint32_t)(left < 16 ? left : 16) : 0u;
-        src.c[r] = make_rsrc((const char*)pb.codes + r0 * rowbytes, rows * rowbytes);
-        src.s[r] = make_rsrc((const char*)pb.scales + r0 * sbrow, rows * sbrow);
-        src.b[r] = make_rsrc((const char*)pb.biases + r0 * sbrow, rows * sbrow);
+        c.cb[r] = (const char*)pb.codes;
+        c.sb[r] = (const char*)pb.scales;
+        c.bb[r] = (const char*)pb.biases;
       }
+    }
+  }
+
+  static JQ_DEV void cursor_at(const DmxArgs& a, int it, Cursor& c, int4* tlo) {
+    c.it = it;
+    if constexpr (GATHER) {
+      c.u = it / a.nrb;
+      c.rb = it - c.u * a.nrb;
+    } else {
+      int u = 0;
+#pragma unroll
+      for (int q = 1; q < jqk::kMaxProblems; ++q)
+        if (q < a.nprob && it >= a.rb_begin[q]) u = q;
+      c.u = u;
+      c.rb = it - a.rb_begin[u];
+    }
+    unit_bases(a, c, tlo);
+  }
+
+  // Returns whether the unit changed.
+  static JQ_DEV bool advance(const DmxArgs& a, Cursor& c, int4* tlo) {
+    ++c.it;
+    if (++c.rb < c.nrb) return false;
+    c.rb = 0;
+    ++c.u;
+    if constexpr (!GATHER) {
+      while (c.u < a.nprob && a.rb_begin[c.u + 1] == a.rb_begin[c.u]) ++c.u;  // empty problems
+    }
+    unit_bases(a, c, tlo);
+    return true;
+  }
+
+  // Buffer views of the cursor's item (0 bytes when dead or empty).
+  static JQ_DEV void sources(const Cursor& c, bool live, uint32_t rowbytes, uint32_t sbrow,
+                             ItemSrc<RT>& src) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      const int64_t r0 = (int64_t)c.rb * IROWS + TSTEP * r;
+      const int64_t left = c.N - r0;
+      const uint32_t rows = live && c.ez && left > 0 ? (uint32_t)(left < 16 ? left : 16) : 0u;
+      src.c[r] = make_rsrc(c.cb[r] + r0 * rowbytes, rows * rowbytes);
+      src.s[r] = make_rsrc(c.sb[r] + r0 * sbrow, rows * sbrow);
+      src.b[r] = make_rsrc(c.bb[r] + r0 * sbrow, rows * sbrow);
     }
   }
 
@@ -408,20 +451,19 @@ struct Dmx {
     Offs o;
     offsets(lane, rowbytes, sbrow, s0, o);
 
-    // Ring prologue: items first .. first + NSLOT - 2.
-    int tile, p;
-    int64_t row0;
+    // Ring prologue: items first .. first + NSLOT - 2 (the copy cursor ends on the next).
+    Cursor cc, wc;  // copy cursor (NSLOT - 1 items ahead) and work cursor
     int4 tl;
-    ItemSrc<RT> src;
+    cursor_at(a, first, wc, &tl);
+    cc = wc;
 #pragma unroll
     for (int k = 0; k < NSLOT - 1; ++k) {
-      const int it = first + k;
-      locate(a, it < end ? it : end - 1, it < end, tile, p, row0, tl, src);
+      ItemSrc<RT> src;
+      sources(cc, cc.it < end, rowbytes, sbrow, src);
       copy(src, o, k == 0 ? ring0 : k == 1 ? ring1 : ring2);  // k < NSLOT - 1 <= 3
       asm volatile("" ::: "memory");
+      advance(a, cc, nullptr);
     }
-    // The first item's own coordinates.
-    locate(a, first, true, tile, p, row0, tl, src);
     Act ac;
     LaneToks<TPL> tk;
     if constexpr (GATHER) {
@@ -435,16 +477,14 @@ struct Dmx {
 
     auto step = [&](int it, JQ_LDS uint8_t* __restrict__ cur, JQ_LDS uint8_t* __restrict__ fill) {
       const int par = (it - first) & 1;  // partials double-buffered across consecutive items
-      // Copy of item it + NSLOT - 1 into the slot freed by item it - 1.
+      // Copy of item it + NSLOT - 1 (the copy cursor) into the slot freed by item it - 1.
       {
-        const int nx = it + NSLOT - 1;
-        int t2, p2;
-        int64_t r2;
-        int4 tl2;
         ItemSrc<RT> s2;
-        locate(a, nx < end ? nx : end - 1, nx < end, t2, p2, r2, tl2, s2);
+        sources(cc, cc.it < end, rowbytes, sbrow, s2);
         copy(s2, o, fill);
+        advance(a, cc, nullptr);
       }
+      const int64_t row0 = (int64_t)wc.rb * IROWS;
       static_assert((NSLOT - 1) * R::ND <= 63, "vmcnt range");
       wait_vm<(NSLOT - 1) * R::ND>();
       asm volatile("" ::: "memory");
@@ -475,8 +515,8 @@ struct Dmx {
           if (w < KW) v += red[((par * KW + w) * NOUT + slot0) * 64 + lane];
         const int tok = ab * TPB + TPL * lg + k;
         if constexpr (GATHER) {
-          const int64_t N = a.g[0].N;
-          const int64_t n = row0 + (NB == 2 ? 0 : 16 * rr) + lr;
+          const int64_t N = wc.N;
+          const int64_t n = row0 + TSTEP * rr + lr;
           if constexpr (NB == 2) {
             float u = 0.f;
             const int slot1 = (ab * RT + 1) * TPL + k;
@@ -493,17 +533,15 @@ struct Dmx {
             if (k == q) orow = tk.orow[q], live = tk.olive[q];
           if (live && n < N) store_out(a.g[0].y, orow * N + n, v, a.yd);
         } else {
-          const QmvProblem& pb = a.b.p[p];
+          const QmvProblem& pb = a.b.p[wc.u < a.nprob ? wc.u : a.nprob - 1];
           const int64_t n = row0 + 16 * rr + lr;
-          if (tok < a.mrows && n < pb.N) store_out(pb.y, (int64_t)(a.m0 + tok) * pb.N + n, v, a.yd);
+          if (tok < a.mrows && n < wc.N) store_out(pb.y, (int64_t)(a.m0 + tok) * wc.N + n, v, a.yd);
         }
       }
-      // Next item's coordinates (and, when its tile differs, its activations).
+      // Next item (and, when its tile differs, its activations).
       if (it + 1 < end) {
-        const int prev = tile;
-        locate(a, it + 1, true, tile, p, row0, tl, src);
-        if constexpr (GATHER) {
-          if (tile != prev) {
+        if (advance(a, wc, &tl)) {
+          if constexpr (GATHER) {
             lane_toks<MP, TPL>(a.plan, tl, lr / D::GSTEP, lg, tk);
             load_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg, [&](int, int64_t& row) { row = tk.xrow; return tk.xlive; }, ac);
           }
