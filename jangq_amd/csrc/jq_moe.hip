@@ -32,7 +32,10 @@ JQ_DEV void argmax_step(float& v, int& id) {
   const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
       __builtin_bit_cast(int, -INFINITY), __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false));
   const int oid = __builtin_amdgcn_update_dpp(0x7FFFFFFF, id, CTRL, ROWS, 0xF, false);
-  if (ov > v || (ov == v && oid < id)) { v = ov; id = oid; }
+  // Bitwise, not short-circuit, logic: selects instead of divergent branches.
+  const bool take = (ov > v) | ((ov == v) & (oid < id));
+  v = take ? ov : v;
+  id = take ? oid : id;
 }
 
 // Wave-wide argmax of (v, id), broadcast to every lane: DPP row operations carry the maximum
@@ -87,15 +90,16 @@ __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ lo
   for (int j = 0; j < k; ++j) {
     float best = -INFINITY;
     int bid = 0x7FFFFFFF;
+    // A lane's ids grow with i, so a strict > keeps the lowest id among its equal values.
 #pragma unroll
     for (int i = 0; i < SL; ++i) {
-      const int e = lane + 64 * i;
-      if (!taken[i] && (v[i] > best || (v[i] == best && e < bid))) { best = v[i]; bid = e; }
+      const bool better = (!taken[i]) & (v[i] > best);
+      best = better ? v[i] : best;
+      bid = better ? lane + 64 * i : bid;
     }
     wave_argmax(best, bid);
 #pragma unroll
-    for (int i = 0; i < SL; ++i)
-      if (lane + 64 * i == bid) taken[i] = true;
+    for (int i = 0; i < SL; ++i) taken[i] = taken[i] | (lane + 64 * i == bid);
     const float p = expf(best - mx) * inv;
     wsum += p;
     if (lane == j) { wsel = p; my_id = bid; }
