@@ -112,6 +112,22 @@ int jq_quantized_matmul(const void* x, int x_dtype, const uint32_t* codes,
                         int y_dtype, jq_stream_t stream);
 
 /*
+ * jq_quantized_matmul with a caller workspace (same reference call: mx.quantized_matmul at
+ * jang-tools/jang_tools/jangrt/linear.py:41-45). Decode batches of long rows (5..64 rows,
+ * K > 4096) split K over the matrix-core kernel and sum fp32 partials in the workspace;
+ * every other shape runs exactly as jq_quantized_matmul. The size query returns the bytes
+ * needed (0: no workspace used, -1: invalid sizes); a smaller workspace returns
+ * JQ_ERR_WORKSPACE.
+ */
+int64_t jq_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int bits,
+                                           int group_size, int x_dtype, int sb_dtype);
+int jq_quantized_matmul_ws(const void* x, int x_dtype, const uint32_t* codes,
+                           const void* scales, const void* biases, int sb_dtype, int bits,
+                           int group_size, int64_t M, int64_t N, int64_t K, void* y,
+                           int y_dtype, void* workspace, int64_t workspace_bytes,
+                           jq_stream_t stream);
+
+/*
  * Grouped form of jq_quantized_matmul: `count` independent problems sharing x_dtype,
  * y_dtype and sb_dtype, in ONE launch when they share M, K, bits and group_size (q/k/v or
  * gate/up projections of one token batch). Each array has `count` entries.

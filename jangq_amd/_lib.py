@@ -24,6 +24,8 @@ SIGNATURES = {
     "jq_quantize": (_I, [_P, _I, _I, _I, _L, _L, _P, _P, _P, _I, _P]),
     "jq_expand_1bit_to_2bit": (_I, [_P, _L, _P, _P]),
     "jq_quantized_matmul": (_I, [_P, _I, _P, _P, _P, _I, _I, _I, _L, _L, _L, _P, _I, _P]),
+    "jq_quantized_matmul_workspace_size": (_L, [_L, _L, _L, _I, _I, _I, _I]),
+    "jq_quantized_matmul_ws": (_I, [_P, _I, _P, _P, _P, _I, _I, _I, _L, _L, _L, _P, _I, _P, _L, _P]),
     "jq_quantized_matmul_multi": (
         _I,
         [_I, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P],

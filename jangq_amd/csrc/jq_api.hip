@@ -133,6 +133,40 @@ int jq_quantized_matmul(const void* x, int x_dtype, const uint32_t* codes, const
                    y_dtype, st);
 }
 
+// Workspace-taking form of jq_quantized_matmul: decode batches (5..64 rows) of long rows
+// (K > 4096) split K over the matrix-core items and sum fp32 partials in the workspace.
+static bool use_split(int64_t M, int64_t N, int64_t K, int bits, int gs, int xd, int sb) {
+  const int Mi = (int)(M < (1 << 30) ? M : (1 << 30));
+  return M > 4 && M <= kDecpMaxRows && !jqk::gemv_ok(Mi, K, N, bits, gs, xd, sb) &&
+         jqk::dmx_split_workspace(Mi, K, N, bits, gs, xd, sb) > 0;
+}
+
+int64_t jq_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int bits,
+                                           int group_size, int x_dtype, int sb_dtype) {
+  if (M < 0 || N < 0 || K < 0) return -1;
+  if (!use_split(M, N, K, bits, group_size, x_dtype, sb_dtype)) return 0;
+  return jqk::dmx_split_workspace((int)M, K, N, bits, group_size, x_dtype, sb_dtype);
+}
+
+int jq_quantized_matmul_ws(const void* x, int x_dtype, const uint32_t* codes, const void* scales,
+                           const void* biases, int sb_dtype, int bits, int group_size, int64_t M,
+                           int64_t N, int64_t K, void* y, int y_dtype, void* workspace,
+                           int64_t workspace_bytes, jq_stream_t stream) {
+  int s = check_dense(x, x_dtype, codes, scales, biases, sb_dtype, bits, group_size, M, N, K, y,
+                      y_dtype);
+  if (s) return s;
+  if (M == 0 || N == 0 || K == 0 || !use_split(M, N, K, bits, group_size, x_dtype, sb_dtype))
+    return jq_quantized_matmul(x, x_dtype, codes, scales, biases, sb_dtype, bits, group_size, M,
+                               N, K, y, y_dtype, stream);
+  jqk::QmvBatch b;
+  b.M = (int)M;
+  b.K = (int)K;
+  b.p[0].x = x; b.p[0].codes = codes; b.p[0].scales = scales; b.p[0].biases = biases;
+  b.p[0].y = y; b.p[0].N = N;
+  return jqk::dmx_split_launch(b, bits, group_size, x_dtype, sb_dtype, y_dtype, workspace,
+                               workspace_bytes, (hipStream_t)stream);
+}
+
 int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
                               const uint32_t* const* codes, const void* const* scales,
                               const void* const* biases, int sb_dtype, const int* bits,

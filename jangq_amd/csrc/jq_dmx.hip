@@ -52,8 +52,11 @@ struct DmxArgs {
   // gathered
   QmmProblem g[2];
   GatherPlan plan;
+  // dense with K split into chunks of `split` steps: fp32 partials [chunk][mrows][N]
+  int split;
+  float* part;
   // both
-  int nrb;     // gathered: row blocks per tile
+  int nrb;     // gathered: row blocks per tile (split: row blocks of the matrix)
   int items;   // dense: total items (gathered: read from the plan)
   int K;
   int yd;
@@ -154,7 +157,9 @@ JQ_DEV void lane_toks(const GatherPlan& pl, int4 tl, int xt, int lg, LaneToks<TP
   }
 }
 
-template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB>
+// SPLIT (dense, one problem): unit u of the item walk is a K chunk of a.split steps; its
+// partial sums go to a.part and a second kernel adds the chunks.
+template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB, bool SPLIT = false>
 struct Dmx {
   using R = Ring<D, RT, SW, NSLOT>;
   static constexpr int BITS = D::BITS, TPB = D::TPB, TPL = 4 / D::GSTEP;
@@ -374,6 +379,20 @@ struct Dmx {
         c.sb[r] = (const char*)pb.scales + e * pb.expert_stride_sb * 2;
         c.bb[r] = (const char*)pb.biases + e * pb.expert_stride_sb * 2;
       }
+    } else if constexpr (SPLIT) {
+      if (tlo) *tlo = make_int4(0, 0, 0, 0);
+      const QmvProblem& pb = a.b.p[0];
+      c.ez = 1;
+      c.N = pb.N;
+      c.nrb = a.nrb;
+      const int64_t cbyte = (int64_t)c.u * a.split * 16 * BITS;  // chunk start inside a row
+      const int64_t sbyte = (int64_t)c.u * a.split * D::GSTEP * 2;
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        c.cb[r] = (const char*)pb.codes + cbyte;
+        c.sb[r] = (const char*)pb.scales + sbyte;
+        c.bb[r] = (const char*)pb.biases + sbyte;
+      }
     } else {
       if (tlo) *tlo = make_int4(0, 0, 0, 0);
       const int u = c.u < a.nprob ? c.u : a.nprob - 1;
@@ -392,7 +411,7 @@ struct Dmx {
 
   static JQ_DEV void cursor_at(const DmxArgs& a, int it, Cursor& c, int4* tlo) {
     c.it = it;
-    if constexpr (GATHER) {
+    if constexpr (GATHER || SPLIT) {
       c.u = it / a.nrb;
       c.rb = it - c.u * a.nrb;
     } else {
@@ -412,7 +431,7 @@ struct Dmx {
     if (++c.rb < c.nrb) return false;
     c.rb = 0;
     ++c.u;
-    if constexpr (!GATHER) {
+    if constexpr (!GATHER && !SPLIT) {
       while (c.u < a.nprob && a.rb_begin[c.u + 1] == a.rb_begin[c.u]) ++c.u;  // empty problems
     }
     unit_bases(a, c, tlo);
@@ -470,7 +489,7 @@ struct Dmx {
       lane_toks<MP, TPL>(a.plan, tl, lr / D::GSTEP, lg, tk);
       load_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg, [&](int, int64_t& row) { row = tk.xrow; return tk.xlive; }, ac);
     } else {
-      load_act((const uint16_t*)a.b.p[0].x, a.K, s0, lr, lg,
+      load_act((const uint16_t*)a.b.p[0].x, a.K, s0 + (SPLIT ? wc.u * a.split : 0), lr, lg,
                [&](int t, int64_t& row) { row = a.m0 + t; return t < a.mrows; }, ac);
     }
     const Bases<D> bs = make_bases<D>();
@@ -533,9 +552,13 @@ struct Dmx {
             if (k == q) orow = tk.orow[q], live = tk.olive[q];
           if (live && n < N) store_out(a.g[0].y, orow * N + n, v, a.yd);
         } else {
-          const QmvProblem& pb = a.b.p[wc.u < a.nprob ? wc.u : a.nprob - 1];
           const int64_t n = row0 + 16 * rr + lr;
-          if (tok < a.mrows && n < wc.N) store_out(pb.y, (int64_t)(a.m0 + tok) * wc.N + n, v, a.yd);
+          if constexpr (SPLIT) {
+            if (tok < a.mrows && n < wc.N) a.part[((int64_t)wc.u * a.mrows + tok) * wc.N + n] = v;
+          } else {
+            const QmvProblem& pb = a.b.p[wc.u < a.nprob ? wc.u : a.nprob - 1];
+            if (tok < a.mrows && n < wc.N) store_out(pb.y, (int64_t)(a.m0 + tok) * wc.N + n, v, a.yd);
+          }
         }
       }
       // Next item (and, when its tile differs, its activations).
@@ -544,6 +567,9 @@ struct Dmx {
           if constexpr (GATHER) {
             lane_toks<MP, TPL>(a.plan, tl, lr / D::GSTEP, lg, tk);
             load_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg, [&](int, int64_t& row) { row = tk.xrow; return tk.xlive; }, ac);
+          } else if constexpr (SPLIT) {
+            load_act((const uint16_t*)a.b.p[0].x, a.K, s0 + wc.u * a.split, lr, lg,
+                     [&](int t, int64_t& row) { row = a.m0 + t; return t < a.mrows; }, ac);
           }
         }
       }
@@ -575,9 +601,9 @@ struct Dmx {
   }
 };
 
-template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB>
+template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB, bool SPLIT>
 __global__ void __launch_bounds__(64 * kMaxKW) dmx_kernel(DmxArgs a) {
-  using K = Dmx<D, SB, RT, NA, SW, NSLOT, GATHER, NB>;
+  using K = Dmx<D, SB, RT, NA, SW, NSLOT, GATHER, NB, SPLIT>;
   using R = typename K::R;
   extern __shared__ __attribute__((aligned(1024))) uint8_t dmx_lds[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -597,11 +623,11 @@ constexpr size_t dmx_lds_bytes(int kw) {
   return (size_t)kw * R::WAVE + (size_t)2 * kw * RT * NA * (4 / D::GSTEP) * 64 * 4;
 }
 
-template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB>
+template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB, bool SPLIT>
 int launch_cfg(DmxArgs& a, int kw, int64_t max_items, hipStream_t st) {
   const size_t lds = dmx_lds_bytes<D, RT, NA, SW, NSLOT>(kw);
   if (lds > (size_t)kLdsMax) return JQ_ERR_SHAPE;
-  auto kern = dmx_kernel<D, SB, RT, NA, SW, NSLOT, GATHER, NB>;
+  auto kern = dmx_kernel<D, SB, RT, NA, SW, NSLOT, GATHER, NB, SPLIT>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)lds) != hipSuccess)
     return JQ_ERR_LAUNCH;
@@ -643,14 +669,15 @@ inline int dmx_sw(int K) {
   return 0;
 }
 
-template <class D, int SB, int RT, int NA, bool GATHER, int NB>
+template <class D, int SB, int RT, int NA, bool GATHER, int NB, bool SPLIT = false>
 int launch_sw(DmxArgs& a, int64_t max_items, hipStream_t st) {
-  const int sw = dmx_sw(a.K);
-  const int kw = sw ? a.K / 128 / sw : 0;
+  const int kc = SPLIT ? a.split * 128 : a.K;  // codes of K one block covers
+  const int sw = dmx_sw(kc);
+  const int kw = sw ? kc / 128 / sw : 0;
   if (sw == 2)
-    return launch_cfg<D, SB, RT, NA, 2, ring_slots<D, RT, NA, 2>(), GATHER, NB>(a, kw, max_items, st);
+    return launch_cfg<D, SB, RT, NA, 2, ring_slots<D, RT, NA, 2>(), GATHER, NB, SPLIT>(a, kw, max_items, st);
   if (sw == 4)
-    return launch_cfg<D, SB, RT, NA, 4, ring_slots<D, RT, NA, 4>(), GATHER, NB>(a, kw, max_items, st);
+    return launch_cfg<D, SB, RT, NA, 4, ring_slots<D, RT, NA, 4>(), GATHER, NB, SPLIT>(a, kw, max_items, st);
   return JQ_ERR_SHAPE;
 }
 
@@ -668,6 +695,8 @@ int dense_t(const QmvBatch& b, int nprob, int yd, hipStream_t st) {
     a.K = b.K;
     a.yd = yd;
     a.nrb = 0;
+    a.split = 0;
+    a.part = nullptr;
     int s;
     constexpr int RT = 1;
     int total = 0;
@@ -683,6 +712,80 @@ int dense_t(const QmvBatch& b, int nprob, int yd, hipStream_t st) {
     if (s) return s;
   }
   return JQ_OK;
+}
+
+// Chunk partials summed in chunk order and rounded: y[m0 + m, n] = sum_c part[c, m, n].
+__global__ void split_sum_kernel(const float* __restrict__ part, int nchunk, int64_t mn,
+                                 void* __restrict__ y, int64_t y0, int yd) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < mn;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float v = 0.f;
+    for (int c = 0; c < nchunk; ++c) v += part[(int64_t)c * mn + i];
+    store_out(y, y0 + i, v, yd);
+  }
+}
+
+// K chunks for a split launch: the fewest chunks of at most 4 * kMaxKW steps, each a whole
+// number of steps per wave. Returns the chunk count (0: no split fits) and its steps.
+inline int split_chunks(int64_t K, int& cs) {
+  const int S = (int)(K / 128);
+  for (int nc = 2; nc <= 64; ++nc) {
+    if (S % nc) continue;
+    cs = S / nc;
+    if (cs <= 4 * kMaxKW && dmx_sw(cs * 128)) return nc;
+  }
+  return 0;
+}
+
+template <int BITS, int GS, int XDT, int SB>
+int split_t(const QmvBatch& b, int yd, float* part, int nchunk, int cs, hipStream_t st) {
+  using D = Dc<BITS, GS, XDT>;
+  const int pass = b.M > D::TPB ? 2 * D::TPB : D::TPB;
+  const int64_t N = b.p[0].N;
+  for (int m0 = 0; m0 < b.M; m0 += pass) {
+    DmxArgs a;
+    a.b = b;
+    a.nprob = 1;
+    a.m0 = m0;
+    a.mrows = b.M - m0 < pass ? b.M - m0 : pass;
+    a.K = b.K;
+    a.yd = JQ_F32;
+    a.split = cs;
+    a.part = part;
+    a.nrb = (int)((N + 15) / 16);
+    a.items = nchunk * a.nrb;
+    for (int i = 0; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = i == 0 ? 0 : a.nrb;
+    int s;
+    if (pass > D::TPB) s = launch_sw<D, SB, 1, 2, false, 1, true>(a, a.items, st);
+    else s = launch_sw<D, SB, 1, 1, false, 1, true>(a, a.items, st);
+    if (s) return s;
+    const int64_t mn = (int64_t)a.mrows * N;
+    const int64_t blocks = (mn + 255) / 256;
+    split_sum_kernel<<<(unsigned)(blocks < 4096 ? blocks : 4096), 256, 0, st>>>(
+        part, nchunk, mn, b.p[0].y, (int64_t)m0 * N, yd);
+    s = jqh::launch_status();
+    if (s) return s;
+  }
+  return JQ_OK;
+}
+
+template <int XDT, int SB>
+int split_bits(int bits, int gs, const QmvBatch& b, int yd, float* part, int nchunk, int cs,
+               hipStream_t st) {
+#define JQ_S(B)                                                                       \
+  switch (gs) {                                                                       \
+    case 64: return split_t<B, 64, XDT, SB>(b, yd, part, nchunk, cs, st);             \
+    default: return split_t<B, 128, XDT, SB>(b, yd, part, nchunk, cs, st);            \
+  }
+  switch (bits) {
+    case 2: JQ_S(2)
+    case 3: JQ_S(3)
+    case 4: JQ_S(4)
+    case 5: JQ_S(5)
+    case 6: JQ_S(6)
+    default: JQ_S(8)
+  }
+#undef JQ_S
 }
 
 template <int XDT, int SB>
@@ -782,6 +885,32 @@ int dmx_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, i
   return dense_bits<JQ_F16, JQ_F16>(bits, gs, b, nprob, yd, st);
 }
 
+int64_t dmx_split_workspace(int M, int64_t K, int64_t N, int bits, int gs, int xd, int sb) {
+  if ((xd != JQ_BF16 && xd != JQ_F16) || sb != xd || (gs != 64 && gs != 128)) return 0;
+  if (bits < 2 || bits > 8 || bits == 7 || M < 1 || N < 1 || N >= ((int64_t)1 << 30)) return 0;
+  if (K <= 4 * kMaxKW * 128 || K % 128 || K > ((int64_t)1 << 20)) return 0;
+  int cs = 0;
+  const int nc = split_chunks(K, cs);
+  if (nc == 0) return 0;
+  const int tpb = 16 / (128 / gs);
+  if (dmx_min_lds(bits, gs, cs * 128, 1, M > tpb ? 2 : 1) > (size_t)kLdsMax) return 0;
+  const int pass = M > tpb ? 2 * tpb : tpb;
+  const int rows = M < pass ? M : pass;
+  return (int64_t)nc * rows * N * 4;
+}
+
+int dmx_split_launch(const QmvBatch& b, int bits, int gs, int xd, int sb, int yd, void* ws,
+                     int64_t ws_bytes, hipStream_t st) {
+  const int64_t need = dmx_split_workspace(b.M, b.K, b.p[0].N, bits, gs, xd, sb);
+  if (need == 0) return JQ_ERR_SHAPE;
+  if (!ws || ws_bytes < need) return JQ_ERR_WORKSPACE;
+  int cs = 0;
+  const int nc = split_chunks(b.K, cs);
+  float* part = (float*)ws;
+  if (xd == JQ_BF16) return split_bits<JQ_BF16, JQ_BF16>(bits, gs, b, yd, part, nc, cs, st);
+  return split_bits<JQ_F16, JQ_F16>(bits, gs, b, yd, part, nc, cs, st);
+}
+
 bool dmx_gather_ok(int64_t N, int64_t K, int bits, int gs, int xd, int sb, int nb) {
   return dmx_ok(1, K, N, bits, gs, xd, sb, nb);
 }
@@ -800,6 +929,8 @@ int dmx_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPla
   a.yd = yd;
   a.nprob = 0;
   a.items = 0;
+  a.split = 0;
+  a.part = nullptr;
   if (xd == JQ_BF16)
     return p2 ? gather_bits<JQ_BF16, JQ_BF16, 2>(bits, gs, a, max_tiles, st)
               : gather_bits<JQ_BF16, JQ_BF16, 1>(bits, gs, a, max_tiles, st);

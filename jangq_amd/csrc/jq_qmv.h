@@ -80,6 +80,11 @@ int dmx_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, i
 // Expert-gathered form: plan tiles (plan.tiles != NULL) of up to dmx_tokens_per_tile rows;
 // with p2, gate (p) and up (p2) rows of each tile give h = silu(g) * u.
 bool dmx_gather_ok(int64_t N, int64_t K, int bits, int gs, int xd, int sb, int nb);
+// Long rows (K > 4096) of one problem: K split into chunks over the items, fp32 partials in a
+// workspace (the returned size, 0 when the split does not apply), then one summing launch.
+int64_t dmx_split_workspace(int M, int64_t K, int64_t N, int bits, int gs, int xd, int sb);
+int dmx_split_launch(const QmvBatch& b, int bits, int gs, int xd, int sb, int yd, void* ws,
+                     int64_t ws_bytes, hipStream_t st);
 int dmx_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPlan& plan,
                       int64_t max_tiles, int bits, int gs, int xd, int sb, int yd,
                       hipStream_t st);

@@ -165,10 +165,20 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     M = math.prod(x.shape[:-1])
     if out is None:
         out = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
-    _lib.check(_lib.lib().jq_quantized_matmul(
-        _ptr(x), _dtype_code(x, "x"), _ptr(w), _ptr(scales), _ptr(biases),
-        _dtype_code(scales, "scales"), bits, group_size, M, N, K, _ptr(out),
-        _dtype_code(out, "output"), _stream()), "quantized_matmul")
+    lib = _lib.lib()
+    xd, sd = _dtype_code(x, "x"), _dtype_code(scales, "scales")
+    # Decode batches of long rows split K over the kernel's items (fp32 partials in a
+    # workspace); the size query is 0 for every other shape.
+    nws = lib.jq_quantized_matmul_workspace_size(M, N, K, bits, group_size, xd, sd)
+    if nws > 0:
+        ws = torch.empty(nws, dtype=torch.uint8, device=x.device)
+        _lib.check(lib.jq_quantized_matmul_ws(
+            _ptr(x), xd, _ptr(w), _ptr(scales), _ptr(biases), sd, bits, group_size, M, N, K,
+            _ptr(out), _dtype_code(out, "output"), _ptr(ws), nws, _stream()), "quantized_matmul")
+        return out
+    _lib.check(lib.jq_quantized_matmul(
+        _ptr(x), xd, _ptr(w), _ptr(scales), _ptr(biases), sd, bits, group_size, M, N, K,
+        _ptr(out), _dtype_code(out, "output"), _stream()), "quantized_matmul")
     return out
 
 

@@ -12,6 +12,7 @@ import pytest
 import torch
 
 import jangq_amd as jq
+from jangq_amd import _lib
 from oracle import jangq_oracle as O
 from tests._util import QWeight, assert_close, codes_tensor, to_tensor, values_of
 
@@ -122,10 +123,40 @@ def test_long_row_decode_batches(bits, gs):
     run_case(6, 30, 8192, bits, gs, xdt="f16", sidecar="f16", seed=bits + gs)
 
 
-@pytest.mark.parametrize("M", [5, 8, 32])
+@pytest.mark.parametrize("M", [5, 8, 16, 32, 64])
 def test_c2_down_projection_batches(M):
-    """Config 2 down projection (4096 x 14336, 2-bit) at decode batches 5, 8 and 32."""
+    """Config 2 down projection (4096 x 14336, 2-bit) at decode batches 5 to 64: K split in
+    chunks over the matrix-core kernel, fp32 partials summed in a workspace."""
     run_case(M, 4096, 14336, 2, 64, seed=900 + M)
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,xdt", [(8, 100, 6144, 3, 64, "bf16"),
+                                               (16, 37, 8192, 6, 128, "f16"),
+                                               (24, 64, 12288, 4, 64, "bf16"),
+                                               (9, 48, 16384, 8, 128, "bf16")])
+def test_long_row_split_k(M, N, K, bits, gs, xdt):
+    """The workspace form directly: chunked K (2 to 4 chunks), ragged N, both passes."""
+    qw = QWeight(N, K, bits, gs, seed=M + K, sidecar=xdt)
+    rng = np.random.default_rng(K + M)
+    x = O.round_to(rng.standard_normal((M, K), dtype=np.float32), xdt)
+    lib = _lib.lib()
+    code = {"bf16": 1, "f16": 2}[xdt]
+    nws = lib.jq_quantized_matmul_workspace_size(M, N, K, bits, gs, code, code)
+    assert nws > 0
+    tx = to_tensor(x, xdt)
+    y = torch.empty((M, N), dtype=tx.dtype, device="cuda")
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+    st = lib.jq_quantized_matmul_ws(tx.data_ptr(), code, qw.dw.data_ptr(), qw.ds.data_ptr(),
+                                    qw.db.data_ptr(), code, bits, gs, M, N, K, y.data_ptr(), code,
+                                    ws.data_ptr(), nws, torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    assert lib.jq_quantized_matmul_ws(tx.data_ptr(), code, qw.dw.data_ptr(), qw.ds.data_ptr(),
+                                      qw.db.data_ptr(), code, bits, gs, M, N, K, y.data_ptr(),
+                                      code, ws.data_ptr(), nws - 1,
+                                      torch.cuda.current_stream().cuda_stream) == -7
+    ref = O.quantized_matmul(x, qw.packed, qw.s, qw.b, bits, gs)
+    assert_close(values_of(y), O.round_to(ref, xdt), f"split-K M{M} K{K} b{bits} g{gs}",
+                 exact=ref, out_dtype=xdt)
 
 
 def test_multi_matches_single():
