@@ -217,6 +217,29 @@ int jq_moe_combine(const void* y, const float* w, const void* shared, int64_t T,
                    int64_t H, void* out, int dtype, jq_stream_t stream);
 
 /*
+ * SwitchGLU followed by the weighted combine, one call for the routed part of a MoE block:
+ *   out[t, :] = jq_moe_combine(jq_switch_glu(x, idx)[t, :, :], weights[t, :], shared[t, :])
+ * with the same values and roundings as those two calls (y_buf [T, k, H] of y_dtype is the
+ * caller scratch for the per-slot expert outputs, weights f32 [T, k], shared [T, H] or NULL,
+ * out [T, H]). At decode sizes the combine runs inside the down-projection launch (one block
+ * sums a row's k expert outputs in slot order), so the routed experts take two launches and
+ * y_buf is not written; elsewhere it is the two calls. An expert id >= E contributes 0 in the
+ * fused form (jq_switch_glu leaves such rows unwritten).
+ * Replaces the routed half of the fused affine MoE decode of
+ * jang-tools/jang_tools/dsv41/metal_decode.py:334-503 (gate|up and down+combine dispatches)
+ * and the caller-side composition of jang-tools/jang_tools/qwen4_exp/modeling.py:594-597.
+ */
+int jq_switch_glu_combine(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
+                          int64_t E, const uint32_t* idx, const float* weights, int k,
+                          const uint32_t* gate_codes, const void* gate_scales,
+                          const void* gate_biases, const uint32_t* up_codes,
+                          const void* up_scales, const void* up_biases, int bits_gu,
+                          const uint32_t* down_codes, const void* down_scales,
+                          const void* down_biases, int bits_d, int sb_dtype, int group_size,
+                          void* h_buf, void* y_buf, const void* shared, void* out, int y_dtype,
+                          void* workspace, int64_t workspace_bytes, jq_stream_t stream);
+
+/*
  * SwiGLU projection pair of a dense MLP: h = silu(round(x @ Wg^T)) * round(x @ Wu^T), each
  * product rounded to y_dtype first (as two quantized_matmul calls returning y_dtype give),
  * h rounded to y_dtype. Gate and up share bits, group size, N and K.

@@ -47,6 +47,12 @@ SIGNATURES = {
          _P, _P, _P, _P, _P, _P, _I,
          _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _L, _P],
     ),
+    "jq_switch_glu_combine": (
+        _I,
+        [_P, _I, _L, _L, _L, _L, _P, _P, _I,
+         _P, _P, _P, _P, _P, _P, _I,
+         _P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _L, _P],
+    ),
 }
 
 _lib: C.CDLL | None = None

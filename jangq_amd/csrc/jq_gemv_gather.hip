@@ -27,6 +27,8 @@ using namespace jqg;
 using jqk::GatherPlan;
 using jqk::QmmProblem;
 
+constexpr int kMaxCombSlots = 16;  // expert slots (waves) of a combined-form block
+
 struct GatherArgs {
   QmmProblem p[2];  // the projection (and up, NB == 2); output and shapes from p[0]
   GatherPlan plan;
@@ -34,12 +36,24 @@ struct GatherArgs {
   int ushift;       // log2(gs / 32)
   int kwshift;      // log2(waves per block)
   int yd;
+  // Combined form (direct pairs t*ck + j, one row each): out[t, n] = round(sum_j cw[t*ck+j] *
+  // y[t*ck+j, n]) (+ cshared[t, n]), the k experts of a token summed in slot order.
+  const float* cw;
+  const void* cshared;
+  void* cout;
+  int ck, ctok;
 };
 
 JQ_DEV float round_out(float v, int yd) {
   if (yd == JQ_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
   if (yd == JQ_F16) return f16_bits_to_f32(f32_to_f16_bits(v));
   return v;
+}
+
+JQ_DEV float load_out(const void* y, int64_t i, int yd) {
+  if (yd == JQ_BF16) return load_t<JQ_BF16>(y, i);
+  if (yd == JQ_F16) return load_t<JQ_F16>(y, i);
+  return load_t<JQ_F32>(y, i);
 }
 
 JQ_DEV void store_out(void* y, int64_t i, float v, int yd) {
@@ -105,24 +119,31 @@ JQ_DEV float group_total(float v) {
 // RW: rows per wave instruction. Rows shorter than 64 lane chunks (RW = 2, 4) split a single
 // wave into RW groups of 64/RW lanes; group g loads item rows g*RBL .. g*RBL + RBL - 1, and a
 // lane keeps the activations of its chunk for every row. RBL: ring slots (rows) per lane.
-template <class D, int SB, int MT, int RBL, int NB, int RW>
-__global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs a) {
+// COMB: the combined form above. Items are (token, row block); wave j of a block computes
+// expert slot j's rows of the item over the whole of K (the waves do not split K), and wave 0
+// sums the k slot outputs of each row in slot order.
+template <class D, int SB, int MT, int RBL, int NB, int RW, bool COMB = false>
+__global__ void __launch_bounds__(64 * (COMB ? kMaxCombSlots : kMaxWaves))
+gemv_gather_kernel(GatherArgs a) {
   constexpr int BITS = D::BITS;
   constexpr int UPL = units_per_chunk<BITS>();
   constexpr int NW = BITS * UPL;
   constexpr int RB = RBL * RW;   // rows of an item (both projections)
   constexpr int ROWS = RB / NB;  // weight rows of one projection per item
   constexpr int CL = 64 / RW;    // lanes per row group
-  __shared__ float red[2][kMaxWaves][RB * MT];
+  __shared__ float red[2][COMB ? kMaxCombSlots : kMaxWaves][RB * MT];
 
   const int ntiles = a.plan.n_tiles ? *a.plan.n_tiles
                                      : (a.plan.direct_pairs + a.plan.direct_rows - 1) / a.plan.direct_rows;
-  const int items = ntiles * a.nrb;
-  const int per = (items + (int)gridDim.x - 1) / (int)gridDim.x;
-  const int first = blockIdx.x * per;
-  const int end = first + per < items ? first + per : items;
+  int first, end;
+  {
+    const int items = (COMB ? a.ctok : ntiles) * a.nrb;
+    const int per = (items + (int)gridDim.x - 1) / (int)gridDim.x;
+    first = blockIdx.x * per;
+    end = first + per < items ? first + per : items;
+  }
   if (first >= end) return;  // whole block
-  const int KW = blockDim.x >> 6;
+  const int KW = COMB ? 1 : blockDim.x >> 6;  // waves over K
   const int K = (int)a.p[0].K;
   const int64_t N = a.p[0].N;
   const int lane = threadIdx.x & 63;
@@ -134,7 +155,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
 
   const int sr = RW == 1 ? 0 : lane / CL;  // row group of the lane
   const int lc = RW == 1 ? lane : lane % CL;
-  const int c = wave * CW + lc;
+  const int c = (COMB ? 0 : wave) * CW + lc;
   const bool act = lc < CW && c < C;
   const int ci = act ? c : 0;
   const uint32_t voff = (uint32_t)ci * (4 * NW);
@@ -191,8 +212,16 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
   };
 
   int it = first;
-  int tile = it / a.nrb;
-  int rbi = it - tile * a.nrb;
+  int tile, rbi;
+  int ct = 0;  // combined form: token of the item
+  if constexpr (COMB) {
+    ct = it / a.nrb;
+    rbi = it - ct * a.nrb;
+    tile = ct * a.ck + wave;  // the wave's expert slot
+  } else {
+    tile = it / a.nrb;
+    rbi = it - tile * a.nrb;
+  }
   int4 tl = get_tile(a.plan, tile);
   TileRows<MT> tr;
   tile_rows<MT>(a.plan, tl, tr);
@@ -212,8 +241,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
   for (int par = 0;; par ^= 1) {
     const bool more = it + 1 < end;
     const bool wrap = rbi + 1 == a.nrb;
-    const int tile2 = more && wrap ? tile + 1 : tile;
+    const int tile2 = more && wrap ? tile + (COMB ? a.ck : 1) : tile;
     const int rbi2 = more ? (wrap ? 0 : rbi + 1) : rbi;
+    const int ct2 = more && wrap ? ct + 1 : ct;
     const int4 tl2 = get_tile(a.plan, tile2);
     const int64_t row02 = (int64_t)rbi2 * ROWS;
     Rsrc rc2[NB], rs2[NB], rb2[NB];
@@ -246,10 +276,23 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         const float v = group_total<RW>(acc[r][m]);
-        if (lc == CL - 1) red[par][wave][(sr * RBL + r) * MT + m] = v;
+        // (an expert id outside the range gives a slot of 0 rows: it contributes 0)
+        if (lc == CL - 1) red[par][wave][(sr * RBL + r) * MT + m] = COMB && tr.nrows == 0 ? 0.f : v;
       }
     __syncthreads();
-    if (wave == 0 && lane < ROWS * MT) {
+    if constexpr (COMB) {
+      // Each slot's output row, rounded as the expert output, joins the token's sum in slot
+      // order (fp32); then round, + shared, store.
+      const int64_t row = row0 + lane;
+      if (wave == 0 && lane < ROWS && row < N) {
+        float comb = 0.f;
+        for (int j = 0; j < a.ck; ++j)
+          comb = fmaf(a.cw[ct * a.ck + j], round_out(red[par][j][lane], a.yd), comb);
+        float r = round_out(comb, a.yd);
+        if (a.cshared) r += load_out(a.cshared, (int64_t)ct * N + row, a.yd);
+        store_out(a.cout, (int64_t)ct * N + row, r, a.yd);
+      }
+    } else if (wave == 0 && lane < ROWS * MT) {
       const int j = lane / MT, m = lane % MT;
       int64_t orow = tr.orow[0];
       bool live = 0 < tr.nrows;
@@ -278,6 +321,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
     it += 1;
     tile = tile2;
     rbi = rbi2;
+    ct = ct2;
     tl = tl2;
     row0 = row02;
 #pragma unroll
@@ -285,11 +329,15 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_gather_kernel(GatherArgs 
   }
 }
 
-template <class D, int SB, int MT, int RBL, int NB, int RW>
+template <class D, int SB, int MT, int RBL, int NB, int RW, bool COMB = false>
 int launch_g(GatherArgs& a, int64_t max_tiles, hipStream_t st) {
   int kws = 0;
-  const int kw = RW == 1 ? gemv_waves(a.p[0].K, D::BITS, &kws) : 1;
+  int kw = RW == 1 ? gemv_waves(a.p[0].K, D::BITS, &kws) : 1;
   if (kw > kMaxWaves) return JQ_ERR_SHAPE;
+  if (COMB) {
+    if (kw != 1 || a.ck > kMaxCombSlots) return JQ_ERR_SHAPE;
+    kw = a.ck;  // one wave per expert slot
+  }
   a.kwshift = kws;
   constexpr int ROWS = RBL * RW / NB;
   const int64_t nrb = (a.p[0].N + ROWS - 1) / ROWS;
@@ -297,17 +345,19 @@ int launch_g(GatherArgs& a, int64_t max_tiles, hipStream_t st) {
   if (nrb == 0 || max_items == 0) return JQ_OK;
   if (max_items >= ((int64_t)1 << 31)) return JQ_ERR_SHAPE;
   a.nrb = (int)nrb;
+  const int64_t units = COMB ? (int64_t)a.ctok * nrb : max_items;  // block ranges
   int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_gather_kernel<D, SB, MT, RBL, NB, RW>,
-                                                   64 * kw, 0) != hipSuccess || nb < 1)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &nb, gemv_gather_kernel<D, SB, MT, RBL, NB, RW, COMB>, 64 * kw, 0) != hipSuccess ||
+      nb < 1)
     nb = 1;
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
   const int64_t cap = (int64_t)nb * cus;
-  const int grid = (int)(max_items < cap ? max_items : cap);
-  gemv_gather_kernel<D, SB, MT, RBL, NB, RW><<<grid, 64 * kw, 0, st>>>(a);
+  const int grid = (int)(units < cap ? units : cap);
+  gemv_gather_kernel<D, SB, MT, RBL, NB, RW, COMB><<<grid, 64 * kw, 0, st>>>(a);
   return jqh::launch_status();
 }
 
@@ -316,6 +366,10 @@ int launch_g(GatherArgs& a, int64_t max_tiles, hipStream_t st) {
 template <class D, int SB, int NB, int RW>
 int launch_rw(GatherArgs& a, int mt, int64_t max_tiles, hipStream_t st) {
   constexpr int RBL = 4 * NB;
+  if (a.cout) {
+    if constexpr (NB == 1) return launch_g<D, SB, 1, RBL, NB, RW, true>(a, max_tiles, st);
+    return JQ_ERR_SHAPE;
+  }
   if (mt == 1) return launch_g<D, SB, 1, RBL, NB, RW>(a, max_tiles, st);
   if (mt == 2) return launch_g<D, SB, 2, RBL, NB, RW>(a, max_tiles, st);
   if constexpr (D::BITS != 2) {
@@ -387,8 +441,41 @@ int gemv_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPl
   a.plan = plan;
   a.ushift = gs == 32 ? 0 : gs == 64 ? 1 : 2;
   a.yd = yd;
+  a.cw = nullptr;
+  a.cshared = nullptr;
+  a.cout = nullptr;
+  a.ck = a.ctok = 0;
   if (p2) return launch_bits<2>(a, bits, xd, sb, tile_rows, max_tiles, st);
   return launch_bits<1>(a, bits, xd, sb, tile_rows, max_tiles, st);
+}
+
+bool gemv_gather_comb_ok(int64_t T, int k, int64_t N, int64_t K, int bits, int gs, int xd,
+                         int sb) {
+  // One wave per slot, each over a whole row: rows of at most 32 lane chunks, or rows that
+  // take a single wave anyway.
+  const int64_t C = K / (bits == 2 ? 64 : 32);
+  return T > 0 && k > 0 && k <= kMaxCombSlots && gemv_gather_ok(N, K, bits, gs, xd, sb) &&
+         (C <= 32 || gemv_waves(K, bits, nullptr) == 1) && T * k < ((int64_t)1 << 20);
+}
+
+int gemv_gather_comb_launch(const QmmProblem& p, const GatherPlan& plan, const float* w,
+                            const void* shared, void* out, int64_t T, int k, int bits, int gs,
+                            int xd, int sb, int yd, hipStream_t st) {
+  if (T == 0 || p.N == 0) return JQ_OK;
+  if (!gemv_gather_comb_ok(T, k, p.N, p.K, bits, gs, xd, sb) || plan.tiles || plan.lhs ||
+      plan.direct_rows != 1 || plan.direct_pairs != T * k || !w || !out)
+    return JQ_ERR_SHAPE;
+  GatherArgs a;
+  a.p[0] = a.p[1] = p;
+  a.plan = plan;
+  a.ushift = gs == 32 ? 0 : gs == 64 ? 1 : 2;
+  a.yd = yd;
+  a.cw = w;
+  a.cshared = shared;
+  a.cout = out;
+  a.ck = k;
+  a.ctok = (int)T;
+  return launch_bits<1>(a, bits, xd, sb, 1, T * k, st);
 }
 
 }  // namespace jqk

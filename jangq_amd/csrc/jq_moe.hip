@@ -528,13 +528,17 @@ int jq_gather_qmm(const void* x, int x_dtype, int64_t x_batch, int64_t M, const 
   return grouped_launch(c, p, nullptr, plan, mt, bits, group_size, x_dtype, sb_dtype, y_dtype, st);
 }
 
-int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E,
-                  const uint32_t* idx, int k, const uint32_t* gate_codes, const void* gate_scales,
-                  const void* gate_biases, const uint32_t* up_codes, const void* up_scales,
-                  const void* up_biases, int bits_gu, const uint32_t* down_codes,
-                  const void* down_scales, const void* down_biases, int bits_d, int sb_dtype,
-                  int group_size, void* h_buf, void* out, int y_dtype, void* workspace,
-                  int64_t workspace_bytes, jq_stream_t stream) {
+// jq_switch_glu, and with comb_out != NULL the combine of jq_moe_combine fused into the down
+// launch where the direct decode form applies (else out is written and combined after).
+static int switch_glu_run(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
+                          int64_t E, const uint32_t* idx, int k, const uint32_t* gate_codes,
+                          const void* gate_scales, const void* gate_biases,
+                          const uint32_t* up_codes, const void* up_scales, const void* up_biases,
+                          int bits_gu, const uint32_t* down_codes, const void* down_scales,
+                          const void* down_biases, int bits_d, int sb_dtype, int group_size,
+                          void* h_buf, void* out, int y_dtype, void* workspace,
+                          int64_t workspace_bytes, const float* cw, const void* cshared,
+                          void* comb_out, hipStream_t st) {
   int s = check_expert_shape(bits_gu, group_size, E, I, H);
   if (s) return s;
   s = check_expert_shape(bits_d, group_size, E, H, I);
@@ -549,8 +553,8 @@ int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, i
   if (!x || !idx || !gate_codes || !gate_scales || !gate_biases || !up_codes || !up_scales ||
       !up_biases || !down_codes || !down_scales || !down_biases || !h_buf || !out)
     return JQ_ERR_NULL;
+  if (comb_out && !cw) return JQ_ERR_NULL;
   if (!workspace || workspace_bytes < ws_layout(n_pairs, E, 1).total) return JQ_ERR_WORKSPACE;
-  hipStream_t st = (hipStream_t)stream;
   // Pair i = t*k + j uses x row t = i / k and expert idx[i]; one plan serves both launches
   // (gate+up reads x rows i / k, down reads h rows i).
   const int bv[2] = {bits_gu, bits_d};
@@ -583,8 +587,43 @@ int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, i
   d.M = 1; d.N = H; d.K = I;
   d.expert_stride_codes = H * (I * bits_d / 32);
   d.expert_stride_sb = H * (I / group_size);
-  return grouped_launch(c, d, nullptr, plan, mt, bits_d, group_size, y_dtype, sb_dtype, y_dtype,
-                        st);
+  if (comb_out && direct &&
+      jqk::gemv_gather_comb_ok(T, k, H, I, bits_d, group_size, y_dtype, sb_dtype))
+    return jqk::gemv_gather_comb_launch(d, plan, cw, cshared, comb_out, T, k, bits_d,
+                                        group_size, y_dtype, sb_dtype, y_dtype, st);
+  s = grouped_launch(c, d, nullptr, plan, mt, bits_d, group_size, y_dtype, sb_dtype, y_dtype, st);
+  if (s || !comb_out) return s;
+  return jq_moe_combine(out, cw, cshared, T, k, H, comb_out, y_dtype, (jq_stream_t)st);
+}
+
+int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E,
+                  const uint32_t* idx, int k, const uint32_t* gate_codes, const void* gate_scales,
+                  const void* gate_biases, const uint32_t* up_codes, const void* up_scales,
+                  const void* up_biases, int bits_gu, const uint32_t* down_codes,
+                  const void* down_scales, const void* down_biases, int bits_d, int sb_dtype,
+                  int group_size, void* h_buf, void* out, int y_dtype, void* workspace,
+                  int64_t workspace_bytes, jq_stream_t stream) {
+  return switch_glu_run(x, x_dtype, T, H, I, E, idx, k, gate_codes, gate_scales, gate_biases,
+                        up_codes, up_scales, up_biases, bits_gu, down_codes, down_scales,
+                        down_biases, bits_d, sb_dtype, group_size, h_buf, out, y_dtype,
+                        workspace, workspace_bytes, nullptr, nullptr, nullptr,
+                        (hipStream_t)stream);
+}
+
+int jq_switch_glu_combine(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
+                          int64_t E, const uint32_t* idx, const float* weights, int k,
+                          const uint32_t* gate_codes, const void* gate_scales,
+                          const void* gate_biases, const uint32_t* up_codes,
+                          const void* up_scales, const void* up_biases, int bits_gu,
+                          const uint32_t* down_codes, const void* down_scales,
+                          const void* down_biases, int bits_d, int sb_dtype, int group_size,
+                          void* h_buf, void* y_buf, const void* shared, void* out, int y_dtype,
+                          void* workspace, int64_t workspace_bytes, jq_stream_t stream) {
+  if (T > 0 && (!weights || !out)) return JQ_ERR_NULL;
+  return switch_glu_run(x, x_dtype, T, H, I, E, idx, k, gate_codes, gate_scales, gate_biases,
+                        up_codes, up_scales, up_biases, bits_gu, down_codes, down_scales,
+                        down_biases, bits_d, sb_dtype, group_size, h_buf, y_buf, y_dtype,
+                        workspace, workspace_bytes, weights, shared, out, (hipStream_t)stream);
 }
 
 }  // extern "C"

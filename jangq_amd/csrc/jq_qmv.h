@@ -129,5 +129,14 @@ bool gemv_gather_ok(int64_t N, int64_t K, int bits, int gs, int xd, int sb);
 int gemv_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPlan& plan,
                        int64_t max_tiles, int tile_rows, int bits, int gs, int xd, int sb,
                        int yd, hipStream_t st);
+// The same GEMV over a direct plan of T * k pairs (pair t*k + j reads x row t*k + j) with the
+// MoE combine fused in: out[t, n] = round(sum_j w[t*k+j] * round(y[t*k+j, n])) (+ shared[t, n]),
+// slot order in fp32; an expert id outside [0, E) contributes 0. One wave per slot (k <= 16),
+// each over whole rows: K of at most 32 lane chunks or of a single wave.
+bool gemv_gather_comb_ok(int64_t T, int k, int64_t N, int64_t K, int bits, int gs, int xd,
+                         int sb);
+int gemv_gather_comb_launch(const QmmProblem& p, const GatherPlan& plan, const float* w,
+                            const void* shared, void* out, int64_t T, int k, int bits, int gs,
+                            int xd, int sb, int yd, hipStream_t st);
 
 }  // namespace jqk

@@ -156,14 +156,17 @@ class SparseMoeBlock(torch.nn.Module):
         if logits is None:
             logits = self.gate(x).float()
         inds, scores = ops.moe_route(logits, self.top_k, self.norm_topk_prob)
-        y = self.switch_mlp(x, inds)
         if side is not None:
             main.wait_stream(side)
             shared.record_stream(main)
         elif self.shared_expert is not None:
             shared = self.shared_expert(x)
-        # (y * scores[..., None]).sum(-2) (+ shared), qwen4_exp/modeling.py:594-597
-        return ops.moe_combine(y, scores, shared)
+        # switch_mlp, then (y * scores[..., None]).sum(-2) (+ shared), qwen4_exp/modeling.py:594-597;
+        # one call, so that at decode sizes the combine runs inside the down-projection launch.
+        m = self.switch_mlp
+        return ops.switch_glu_combine(x, inds, scores, m.gate_proj.as_tuple(),
+                                      m.up_proj.as_tuple(), m.down_proj.as_tuple(),
+                                      m.gate_proj.group_size, shared)
 
     _streams: dict = {}
 

@@ -329,6 +329,56 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, down, group_siz
     return out
 
 
+def switch_glu_combine(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tensor, gate, up,
+                       down, group_size: int = 64,
+                       shared: torch.Tensor | None = None) -> torch.Tensor:
+    """moe_combine(switch_glu(x, indices, gate, up, down), weights, shared) as one call: the
+    routed half of a MoE block (qwen4_exp/modeling.py:594-597; the two-dispatch fused decode
+    of dsv41/metal_decode.py:334-503). Same values and roundings as the two calls; at decode
+    sizes the combine runs inside the down-projection launch."""
+    x = _dev(x, "x")
+    indices = _dev(indices, "indices")
+    gw, gsc, gb, bits_gu = gate
+    uw, usc, ub, bits_u = up
+    dw, dsc, db, bits_d = down
+    if bits_u != bits_gu:
+        raise ValueError("gate and up projections must share a bit width")
+    _check_bits_gs(bits_gu, group_size)
+    _check_bits_gs(bits_d, group_size)
+    gw, uw, dw = _codes(gw), _codes(uw), _codes(dw)
+    E, I = gw.shape[0], gw.shape[1]
+    H = x.shape[-1]
+    k = indices.shape[-1]
+    if packed_in_features(gw, bits_gu) != H or dw.shape[1] != H or packed_in_features(dw, bits_d) != I:
+        raise ValueError("expert weight shapes do not match x / each other")
+    T = math.prod(x.shape[:-1])
+    if math.prod(indices.shape[:-1]) != T:
+        raise ValueError("indices leading dims must match x")
+    w = _dev(weights, "weights")
+    if tuple(w.shape) != tuple(indices.shape):
+        raise ValueError(f"weights must be {tuple(indices.shape)}, got {tuple(w.shape)}")
+    w = w.reshape(T, k).float().contiguous()
+    if shared is not None:
+        shared = _dev(shared, "shared")
+        if tuple(shared.shape) != tuple(x.shape) or shared.dtype != x.dtype:
+            raise ValueError("shared must match x's shape and dtype")
+        shared = shared.contiguous()
+    idx = indices.reshape(T, k).to(torch.int32).contiguous()
+    h = torch.empty((T * k, I), dtype=x.dtype, device=x.device)
+    ybuf = torch.empty((T * k, H), dtype=x.dtype, device=x.device)
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    ws = _gather_workspace(T * k, E, 1, x.device)
+    sdt = _dtype_code(gsc, "scales")
+    _lib.check(_lib.lib().jq_switch_glu_combine(
+        _ptr(x), _dtype_code(x, "x"), T, H, I, E, _ptr(idx), _ptr(w), k,
+        _ptr(gw), _ptr(_dev(gsc, "scales")), _ptr(_dev(gb, "biases")),
+        _ptr(uw), _ptr(_dev(usc, "scales")), _ptr(_dev(ub, "biases")), bits_gu,
+        _ptr(dw), _ptr(_dev(dsc, "scales")), _ptr(_dev(db, "biases")), bits_d, sdt, group_size,
+        _ptr(h), _ptr(ybuf), _ptr(shared), _ptr(out), _dtype_code(out, "output"), _ptr(ws),
+        ws.numel(), _stream()), "switch_glu_combine")
+    return out
+
+
 def moe_combine(y: torch.Tensor, weights: torch.Tensor,
                 shared: torch.Tensor | None = None) -> torch.Tensor:
     """sum_j weights[..., j] * y[..., j, :] in fp32 (slot order), in y.dtype, plus ``shared``
