@@ -144,35 +144,16 @@ class SparseMoeBlock(torch.nn.Module):
         return ops.moe_route(logits, self.top_k, self.norm_topk_prob)
 
     def forward(self, x: torch.Tensor, logits: torch.Tensor | None = None) -> torch.Tensor:
-        # The shared expert does not depend on the routing: it runs on a second stream (same
-        # priority) so that its launches overlap the router, top-k and expert launches.
-        shared, side = None, None
-        if self.shared_expert is not None and x.is_cuda:
-            main = torch.cuda.current_stream(x.device)
-            side = self._side_stream(x.device)
-            side.wait_stream(main)
-            with torch.cuda.stream(side):
-                shared = self.shared_expert(x)
+        # One stream: the shared expert first, so that its output is ready for the launch that
+        # combines the routed experts. (A second stream for it measured no faster inside a HIP
+        # graph, whose replay ran the two branches one after the other, and much slower eagerly.)
+        shared = self.shared_expert(x) if self.shared_expert is not None else None
         if logits is None:
             logits = self.gate(x).float()
         inds, scores = ops.moe_route(logits, self.top_k, self.norm_topk_prob)
-        if side is not None:
-            main.wait_stream(side)
-            shared.record_stream(main)
-        elif self.shared_expert is not None:
-            shared = self.shared_expert(x)
         # switch_mlp, then (y * scores[..., None]).sum(-2) (+ shared), qwen4_exp/modeling.py:594-597;
         # one call, so that at decode sizes the combine runs inside the down-projection launch.
         m = self.switch_mlp
         return ops.switch_glu_combine(x, inds, scores, m.gate_proj.as_tuple(),
                                       m.up_proj.as_tuple(), m.down_proj.as_tuple(),
                                       m.gate_proj.group_size, shared)
-
-    _streams: dict = {}
-
-    @classmethod
-    def _side_stream(cls, device) -> torch.cuda.Stream:
-        key = torch.device(device).index
-        if key not in cls._streams:
-            cls._streams[key] = torch.cuda.Stream(device=device)  # default priority
-        return cls._streams[key]
