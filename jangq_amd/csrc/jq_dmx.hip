@@ -48,11 +48,12 @@ struct DmxArgs {
   QmvBatch b;
   int rb_begin[jqk::kMaxProblems + 1];
   int nprob;
-  int m0, mrows;
+  int mpass, mtotal;  // activation rows per pass (blockIdx.y is the pass) and in all
+
   // gathered
   QmmProblem g[2];
   GatherPlan plan;
-  // dense with K split into chunks of `split` steps: fp32 partials [chunk][mrows][N]
+  // dense with K split into chunks of `split` steps: fp32 partials [chunk][mtotal][N]
   int split;
   float* part;
   // both
@@ -465,6 +466,9 @@ struct Dmx {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lr = lane & 15, lg = lane >> 4;
     const int s0 = wave * SW;
+    // Dense: the pass of this block (all passes share the weights, read again from the cache).
+    const int pm0 = GATHER ? 0 : (int)blockIdx.y * a.mpass;
+    const int pmr = GATHER ? 0 : (a.mtotal - pm0 < a.mpass ? a.mtotal - pm0 : a.mpass);
     const uint32_t rowbytes = (uint32_t)(a.K / 32) * BITS * 4;
     const uint32_t sbrow = (uint32_t)(a.K / D::GS) * 2;
     Offs o;
@@ -490,7 +494,7 @@ struct Dmx {
       load_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg, [&](int, int64_t& row) { row = tk.xrow; return tk.xlive; }, ac);
     } else {
       load_act((const uint16_t*)a.b.p[0].x, a.K, s0 + (SPLIT ? wc.u * a.split : 0), lr, lg,
-               [&](int t, int64_t& row) { row = a.m0 + t; return t < a.mrows; }, ac);
+               [&](int t, int64_t& row) { row = pm0 + t; return t < pmr; }, ac);
     }
     const Bases<D> bs = make_bases<D>();
 
@@ -554,10 +558,10 @@ struct Dmx {
         } else {
           const int64_t n = row0 + 16 * rr + lr;
           if constexpr (SPLIT) {
-            if (tok < a.mrows && n < wc.N) a.part[((int64_t)wc.u * a.mrows + tok) * wc.N + n] = v;
+            if (tok < pmr && n < wc.N) a.part[((int64_t)wc.u * a.mtotal + pm0 + tok) * wc.N + n] = v;
           } else {
             const QmvProblem& pb = a.b.p[wc.u < a.nprob ? wc.u : a.nprob - 1];
-            if (tok < a.mrows && n < wc.N) store_out(pb.y, (int64_t)(a.m0 + tok) * wc.N + n, v, a.yd);
+            if (tok < pmr && n < wc.N) store_out(pb.y, (int64_t)(pm0 + tok) * wc.N + n, v, a.yd);
           }
         }
       }
@@ -569,7 +573,7 @@ struct Dmx {
             load_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg, [&](int, int64_t& row) { row = tk.xrow; return tk.xlive; }, ac);
           } else if constexpr (SPLIT) {
             load_act((const uint16_t*)a.b.p[0].x, a.K, s0 + wc.u * a.split, lr, lg,
-                     [&](int t, int64_t& row) { row = a.m0 + t; return t < a.mrows; }, ac);
+                     [&](int t, int64_t& row) { row = pm0 + t; return t < pmr; }, ac);
           }
         }
       }
@@ -638,16 +642,20 @@ int launch_cfg(DmxArgs& a, int kw, int64_t max_items, hipStream_t st) {
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
-  const int64_t cap = (int64_t)nb * cus;
+  int64_t cap = (int64_t)nb * cus;
   int64_t grid;
+  int ny = 1;
   if constexpr (GATHER) {
     grid = max_items < cap ? max_items : cap;  // items are read from the plan on the device
   } else {
+    // Passes of activation rows side by side (grid y), sharing the resident-block capacity.
+    ny = (a.mtotal + a.mpass - 1) / a.mpass;
+    cap = cap / ny > 0 ? cap / ny : 1;
     const int64_t iters = (max_items + cap - 1) / cap;
     grid = (max_items + iters - 1) / iters;
   }
-  if (grid < 1) return JQ_OK;
-  kern<<<(unsigned)grid, 64 * kw, lds, st>>>(a);
+  if (grid < 1 || ny < 1) return JQ_OK;
+  kern<<<dim3((unsigned)grid, (unsigned)ny), 64 * kw, lds, st>>>(a);
   return jqh::launch_status();
 }
 
@@ -681,37 +689,32 @@ int launch_sw(DmxArgs& a, int64_t max_items, hipStream_t st) {
   return JQ_ERR_SHAPE;
 }
 
-// Dense: passes of TPB (one activation block) or 2 TPB rows.
+// Dense: passes of TPB (one activation block) or 2 TPB rows, all in one launch.
 template <int BITS, int GS, int XDT, int SB>
 int dense_t(const QmvBatch& b, int nprob, int yd, hipStream_t st) {
   using D = Dc<BITS, GS, XDT>;
+  constexpr int RT = 1;
   const int pass = b.M > D::TPB ? 2 * D::TPB : D::TPB;
-  for (int m0 = 0; m0 < b.M; m0 += pass) {
-    DmxArgs a;
-    a.b = b;
-    a.nprob = nprob;
-    a.m0 = m0;
-    a.mrows = b.M - m0 < pass ? b.M - m0 : pass;
-    a.K = b.K;
-    a.yd = yd;
-    a.nrb = 0;
-    a.split = 0;
-    a.part = nullptr;
-    int s;
-    constexpr int RT = 1;
-    int total = 0;
-    for (int i = 0; i < nprob; ++i) {
-      a.rb_begin[i] = total;
-      total += (int)((b.p[i].N + 16 * RT - 1) / (16 * RT));
-    }
-    for (int i = nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
-    a.items = total;
-    if (total == 0) return JQ_OK;
-    if (pass > D::TPB) s = launch_sw<D, SB, RT, 2, false, 1>(a, total, st);
-    else s = launch_sw<D, SB, RT, 1, false, 1>(a, total, st);
-    if (s) return s;
+  DmxArgs a;
+  a.b = b;
+  a.nprob = nprob;
+  a.mpass = pass;
+  a.mtotal = b.M;
+  a.K = b.K;
+  a.yd = yd;
+  a.nrb = 0;
+  a.split = 0;
+  a.part = nullptr;
+  int total = 0;
+  for (int i = 0; i < nprob; ++i) {
+    a.rb_begin[i] = total;
+    total += (int)((b.p[i].N + 16 * RT - 1) / (16 * RT));
   }
-  return JQ_OK;
+  for (int i = nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
+  a.items = total;
+  if (total == 0) return JQ_OK;
+  if (pass > D::TPB) return launch_sw<D, SB, RT, 2, false, 1>(a, total, st);
+  return launch_sw<D, SB, RT, 1, false, 1>(a, total, st);
 }
 
 // Chunk partials summed in chunk order and rounded: y[m0 + m, n] = sum_c part[c, m, n].
@@ -742,31 +745,27 @@ int split_t(const QmvBatch& b, int yd, float* part, int nchunk, int cs, hipStrea
   using D = Dc<BITS, GS, XDT>;
   const int pass = b.M > D::TPB ? 2 * D::TPB : D::TPB;
   const int64_t N = b.p[0].N;
-  for (int m0 = 0; m0 < b.M; m0 += pass) {
-    DmxArgs a;
-    a.b = b;
-    a.nprob = 1;
-    a.m0 = m0;
-    a.mrows = b.M - m0 < pass ? b.M - m0 : pass;
-    a.K = b.K;
-    a.yd = JQ_F32;
-    a.split = cs;
-    a.part = part;
-    a.nrb = (int)((N + 15) / 16);
-    a.items = nchunk * a.nrb;
-    for (int i = 0; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = i == 0 ? 0 : a.nrb;
-    int s;
-    if (pass > D::TPB) s = launch_sw<D, SB, 1, 2, false, 1, true>(a, a.items, st);
-    else s = launch_sw<D, SB, 1, 1, false, 1, true>(a, a.items, st);
-    if (s) return s;
-    const int64_t mn = (int64_t)a.mrows * N;
-    const int64_t blocks = (mn + 255) / 256;
-    split_sum_kernel<<<(unsigned)(blocks < 4096 ? blocks : 4096), 256, 0, st>>>(
-        part, nchunk, mn, b.p[0].y, (int64_t)m0 * N, yd);
-    s = jqh::launch_status();
-    if (s) return s;
-  }
-  return JQ_OK;
+  DmxArgs a;
+  a.b = b;
+  a.nprob = 1;
+  a.mpass = pass;
+  a.mtotal = b.M;
+  a.K = b.K;
+  a.yd = JQ_F32;
+  a.split = cs;
+  a.part = part;
+  a.nrb = (int)((N + 15) / 16);
+  a.items = nchunk * a.nrb;
+  for (int i = 0; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = i == 0 ? 0 : a.nrb;
+  int s;
+  if (pass > D::TPB) s = launch_sw<D, SB, 1, 2, false, 1, true>(a, a.items, st);
+  else s = launch_sw<D, SB, 1, 1, false, 1, true>(a, a.items, st);
+  if (s) return s;
+  const int64_t mn = (int64_t)b.M * N;
+  const int64_t blocks = (mn + 255) / 256;
+  split_sum_kernel<<<(unsigned)(blocks < 4096 ? blocks : 4096), 256, 0, st>>>(part, nchunk, mn,
+                                                                              b.p[0].y, 0, yd);
+  return jqh::launch_status();
 }
 
 template <int XDT, int SB>
@@ -894,9 +893,7 @@ int64_t dmx_split_workspace(int M, int64_t K, int64_t N, int bits, int gs, int x
   if (nc == 0) return 0;
   const int tpb = 16 / (128 / gs);
   if (dmx_min_lds(bits, gs, cs * 128, 1, M > tpb ? 2 : 1) > (size_t)kLdsMax) return 0;
-  const int pass = M > tpb ? 2 * tpb : tpb;
-  const int rows = M < pass ? M : pass;
-  return (int64_t)nc * rows * N * 4;
+  return (int64_t)nc * M * N * 4;  // fp32 partials of every chunk and activation row
 }
 
 int dmx_split_launch(const QmvBatch& b, int bits, int gs, int xd, int sb, int yd, void* ws,
