@@ -11,6 +11,7 @@
 #include <math.h>
 
 #include "jq_common.h"
+#include "jq_gemv.h"
 #include "jq_qmv.h"
 
 namespace {
@@ -25,35 +26,59 @@ constexpr int kGemmTileRows = 16;
 constexpr int64_t kGemvRows = 4096;
 constexpr int kMaxExperts = 4096;
 
-// One step of the wave argmax: (v, id) against the DPP-moved (v, id) of another lane (lanes
-// outside row_mask keep theirs); larger value wins, ties go to the lower id.
+// Order-preserving u32 key of a float (a larger float has a larger key; -0 is taken as +0
+// by the caller); 0 lies below every float's key and marks chosen or padding slots.
+JQ_DEV uint32_t ord_key(float v) {
+  const uint32_t b = __float_as_uint(v);
+  return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+}
+JQ_DEV float ord_val(uint32_t k) {
+  return __uint_as_float(k & 0x80000000u ? k ^ 0x80000000u : ~k);
+}
+
+// One DPP step of a wave maximum (lanes outside row_mask, and lanes whose source is out of
+// range, see the neutral value and keep theirs).
 template <int CTRL, int ROWS>
-JQ_DEV void argmax_step(float& v, int& id) {
-  const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-      __builtin_bit_cast(int, -INFINITY), __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false));
-  const int oid = __builtin_amdgcn_update_dpp(0x7FFFFFFF, id, CTRL, ROWS, 0xF, false);
-  // Bitwise, not short-circuit, logic: selects instead of divergent branches.
-  const bool take = (ov > v) | ((ov == v) & (oid < id));
-  v = take ? ov : v;
-  id = take ? oid : id;
+JQ_DEV uint64_t max_step(uint64_t k) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)k, CTRL, ROWS, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(k >> 32), CTRL, ROWS, 0xF, false);
+  const uint64_t o = ((uint64_t)hi << 32) | lo;
+  return o > k ? o : k;
+}
+template <int CTRL, int ROWS>
+JQ_DEV float fmax_step(float v) {
+  return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                      __builtin_bit_cast(int, -INFINITY), __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false)));
 }
 
-// Wave-wide argmax of (v, id), broadcast to every lane: DPP row operations carry the maximum
-// into lane 63 (as a wave sum would), a scalar read hands it to all lanes.
-JQ_DEV void wave_argmax(float& v, int& id) {
-  argmax_step<0xB1, 0xF>(v, id);   // quad_perm 1,0,3,2
-  argmax_step<0x4E, 0xF>(v, id);   // quad_perm 2,3,0,1
-  argmax_step<0x124, 0xF>(v, id);  // row_ror 4
-  argmax_step<0x128, 0xF>(v, id);  // row_ror 8
-  argmax_step<0x142, 0xA>(v, id);  // row_bcast 15
-  argmax_step<0x143, 0xC>(v, id);  // row_bcast 31
-  v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-  id = __builtin_amdgcn_readlane(id, 63);
+// Wave maxima, broadcast to every lane: DPP row operations carry the maximum into lane 63
+// (as a wave sum would), a scalar read hands it to all lanes.
+JQ_DEV uint64_t wave_max_u64(uint64_t k) {
+  k = max_step<0xB1, 0xF>(k);   // quad_perm 1,0,3,2
+  k = max_step<0x4E, 0xF>(k);   // quad_perm 2,3,0,1
+  k = max_step<0x124, 0xF>(k);  // row_ror 4
+  k = max_step<0x128, 0xF>(k);  // row_ror 8
+  k = max_step<0x142, 0xA>(k);  // row_bcast 15
+  k = max_step<0x143, 0xC>(k);  // row_bcast 31
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)k, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+JQ_DEV float wave_max_f32(float v) {
+  v = fmax_step<0xB1, 0xF>(v);
+  v = fmax_step<0x4E, 0xF>(v);
+  v = fmax_step<0x124, 0xF>(v);
+  v = fmax_step<0x128, 0xF>(v);
+  v = fmax_step<0x142, 0xA>(v);
+  v = fmax_step<0x143, 0xC>(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-// One wave per token. Lane l holds logits l, l + 64, ... (SL = ceil(E/64) of them) in
-// registers; top-k by k rounds of wave argmax (ties -> lowest expert id), probabilities from a
-// max-subtracted fp32 softmax.
+// One wave per token. Lane l holds the order keys of logits l, l + 64, ... (SL = ceil(E/64)
+// of them); probabilities from a max-subtracted fp32 softmax. Top-k in k rounds on the
+// logits (softmax is monotone): each lane offers its largest remaining key and the wave
+// maximum of (key, ~id) picks the round's expert (ties -> lowest id), whose key is then
+// cleared. Lane j keeps round j's pick; the k probabilities are formed at the end.
 template <int SL>
 __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ logits, int T, int E,
                                                     int k, int renorm, uint32_t* __restrict__ idx,
@@ -62,51 +87,48 @@ __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ lo
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const float* row = logits + (int64_t)t * E;
-  float v[SL];
+  uint32_t key[SL];
+  float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < SL; ++i) {
     const int e = lane + 64 * i;
-    v[i] = e < E ? row[e] : -INFINITY;
+    const float v = e < E ? row[e] + 0.0f : -INFINITY;  // + 0: -0 becomes +0
+    key[i] = e < E ? ord_key(v) : 0u;
+    mx = fmaxf(mx, v);
   }
-  float mx = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < SL; ++i) mx = fmaxf(mx, v[i]);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  mx = wave_max_f32(mx);
   float sum = 0.f;
 #pragma unroll
-  for (int i = 0; i < SL; ++i) sum += lane + 64 * i < E ? expf(v[i] - mx) : 0.f;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  for (int i = 0; i < SL; ++i) sum += key[i] ? expf(ord_val(key[i]) - mx) : 0.f;
+  sum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                      __builtin_bit_cast(int, jqg::wave_total_lane63(sum)), 63));
   const float inv = 1.0f / sum;
 
-  // Selection runs on the logits (softmax is monotone); a chosen slot is set to -inf and
-  // excluded by id (a chosen -inf logit cannot be picked twice).
-  bool taken[SL];
-#pragma unroll
-  for (int i = 0; i < SL; ++i) taken[i] = lane + 64 * i >= E;
-  float wsum = 0.f, wsel = 0.f;
-  int my_id = 0;
+  uint64_t mine = 0;  // lane j: round j's (key, ~id)
   for (int j = 0; j < k; ++j) {
-    float best = -INFINITY;
-    int bid = 0x7FFFFFFF;
-    // A lane's ids grow with i, so a strict > keeps the lowest id among its equal values.
+    // The lane's largest remaining key; a strict > in slot order keeps the lowest id.
+    uint32_t bk = 0;
+    int bi = 0;
 #pragma unroll
     for (int i = 0; i < SL; ++i) {
-      const bool better = (!taken[i]) & (v[i] > best);
-      best = better ? v[i] : best;
-      bid = better ? lane + 64 * i : bid;
+      const bool better = key[i] > bk;
+      bk = better ? key[i] : bk;
+      bi = better ? i : bi;
     }
-    wave_argmax(best, bid);
+    const uint64_t offer = bk ? ((uint64_t)bk << 32) | (uint32_t)~(uint32_t)(lane + 64 * bi) : 0ull;
+    const uint64_t best = wave_max_u64(offer);
+    const uint32_t bid = ~(uint32_t)best;
 #pragma unroll
-    for (int i = 0; i < SL; ++i) taken[i] = taken[i] | (lane + 64 * i == bid);
-    const float p = expf(best - mx) * inv;
-    wsum += p;
-    if (lane == j) { wsel = p; my_id = bid; }
+    for (int i = 0; i < SL; ++i) key[i] = (uint32_t)(lane + 64 * i) == bid ? 0u : key[i];
+    mine = lane == j ? best : mine;
   }
+  const float p = expf(ord_val((uint32_t)(mine >> 32)) - mx) * inv;
+  float wsum = 0.f;  // the k probabilities in round order
+  for (int j = 0; j < k; ++j)
+    wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), j));
   if (lane < k) {
-    idx[(int64_t)t * k + lane] = (uint32_t)my_id;
-    wout[(int64_t)t * k + lane] = renorm ? wsel / wsum : wsel;
+    idx[(int64_t)t * k + lane] = ~(uint32_t)mine;
+    wout[(int64_t)t * k + lane] = renorm ? p / wsum : p;
   }
 }
 
