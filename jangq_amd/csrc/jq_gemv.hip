@@ -201,6 +201,20 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_kernel(GemvArgs a) {
   }
 }
 
+// Blocks of gemv_kernel<D, SB, MT, RB> (kw waves) the GPU holds at once.
+template <class D, int SB, int MT, int RB>
+int64_t resident_blocks(int kw) {
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_kernel<D, SB, MT, RB>, 64 * kw, 0) !=
+          hipSuccess || nb < 1)
+    nb = 1;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  return (int64_t)nb * cus;
+}
+
 // Grid: as many blocks as fit the GPU at once, but no more than there are row blocks, with
 // the row blocks spread evenly (every block takes the same number, up to one).
 template <class D, int SB, int MT, int RB>
@@ -216,15 +230,7 @@ int launch_rb(GemvArgs& a, hipStream_t st) {
   }
   for (int i = a.nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
   if (total == 0) return JQ_OK;
-  int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_kernel<D, SB, MT, RB>, 64 * kw, 0) !=
-          hipSuccess || nb < 1)
-    nb = 1;
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 256;
-  const int64_t cap = (int64_t)nb * cus;
+  const int64_t cap = resident_blocks<D, SB, MT, RB>(kw);
   const int64_t iters = (total + cap - 1) / cap;
   const int grid = (int)((total + iters - 1) / iters);
   gemv_kernel<D, SB, MT, RB><<<grid, 64 * kw, 0, st>>>(a);
@@ -234,12 +240,23 @@ int launch_rb(GemvArgs& a, hipStream_t st) {
 // Rows per block (the ring depth). Measured on MI355X: short rows (one or two waves per
 // block) do best with 4 rows, long rows (four or more waves, e.g. a 14336-wide down
 // projection) with 16; M = 4 keeps 4 rows for registers (18 per unit and token go to x).
+// At 5 and 6 bits (lane chunks of 20 / 24 bytes, two loads per row) short rows whose 4-row
+// blocks would all be resident at once take 2 rows, so that each block walks two or more:
+// config-2 q|k|v (6144 x 4096, 6-bit) 8.0 -> 7.4 us, o (4096 x 4096) 6.01 -> 5.96 us. At
+// 4 bits the same change was slower (4096 x 4096: 5.4 -> 5.7 us), as for long outputs
+// (3-bit gate|up 14.2 -> 15.2 us).
 template <class D, int SB>
 int launch_m(GemvArgs& a, hipStream_t st) {
   constexpr bool two = D::BITS == 2;  // two units per lane chunk
   const bool long_rows = gemv_waves(a.b.K, D::BITS, nullptr) >= 4;
   if (a.b.M == 1) {
     if (long_rows) return launch_rb<D, SB, 1, 16>(a, st);
+    if constexpr (D::BITS == 5 || D::BITS == 6) {
+      int64_t rows = 0;
+      for (int i = 0; i < a.nprob; ++i) rows += a.b.p[i].N;
+      if ((rows + 3) / 4 <= resident_blocks<D, SB, 1, 4>(gemv_waves(a.b.K, D::BITS, nullptr)))
+        return launch_rb<D, SB, 1, 2>(a, st);
+    }
     return launch_rb<D, SB, 1, 4>(a, st);
   }
   if (a.b.M == 2) return launch_rb<D, SB, 2, 4>(a, st);
