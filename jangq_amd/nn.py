@@ -98,9 +98,16 @@ class SwitchGLU(torch.nn.Module):
         self.down_proj = QuantizedSwitchLinear(hidden_dims, input_dims, num_experts,
                                                bits=down_bits or bits, **kw)
 
+    def group_size(self) -> int:
+        """The one group size the three projections share (the SwitchGLU launches take one)."""
+        gs = {self.gate_proj.group_size, self.up_proj.group_size, self.down_proj.group_size}
+        if len(gs) != 1:
+            raise ValueError(f"SwitchGLU projections have different group sizes {sorted(gs)}")
+        return self.gate_proj.group_size
+
     def forward(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         return ops.switch_glu(x, indices, self.gate_proj.as_tuple(), self.up_proj.as_tuple(),
-                              self.down_proj.as_tuple(), self.gate_proj.group_size)
+                              self.down_proj.as_tuple(), self.group_size())
 
 
 class SharedExpertMLP(torch.nn.Module):
@@ -156,4 +163,4 @@ class SparseMoeBlock(torch.nn.Module):
         m = self.switch_mlp
         return ops.switch_glu_combine(x, inds, scores, m.gate_proj.as_tuple(),
                                       m.up_proj.as_tuple(), m.down_proj.as_tuple(),
-                                      m.gate_proj.group_size, shared)
+                                      m.group_size(), shared)

@@ -1,0 +1,75 @@
+"""A JANG v2 bundle loaded onto the GPU modules and run: the 1-bit storage expansion of a
+manifest-listed expert stack (bit-exact to the oracle's), the bits / group-size fix, and the
+loaded MoE block's output against the oracle's composition."""
+import numpy as np
+import pytest
+import torch
+
+from jangq_amd import loader
+from jangq_amd import nn as jnn
+from oracle import jangq_oracle as O
+from tests._util import assert_close, to_tensor, values_of
+from tests.bundle_util import quantized, tensors_of, write_bundle
+
+pytestmark = pytest.mark.gpu
+
+H, I, E, K_TOP = 256, 128, 8, 2
+
+
+def test_loaded_block_matches_oracle(tmp_path):
+    q = {"gate": quantized(E, H, 8, 64, 1),
+         "switch_mlp.gate_proj": quantized(I, H, 3, 128, 2, experts=E),
+         "switch_mlp.up_proj": quantized(I, H, 3, 128, 3, experts=E),
+         "shared_expert.gate_proj": quantized(256, H, 8, 64, 5),
+         "shared_expert.up_proj": quantized(256, H, 8, 64, 6),
+         "shared_expert.down_proj": quantized(H, 256, 8, 64, 7)}
+    t = {}
+    for name, (p, s, b) in q.items():
+        t.update(tensors_of(name, p, s, b))
+    # down stack stored as 1-bit codes (manifest), with 2-bit-range scales and biases
+    rng = np.random.default_rng(11)
+    one = rng.integers(0, 2**32, (E, H, I // 32), dtype=np.uint64).astype(np.uint32)
+    _, ds, db = quantized(H, I, 2, 128, 4, experts=E)
+    t.update(tensors_of("switch_mlp.down_proj", one, ds, db))
+    write_bundle(tmp_path, t, manifest={"switch_mlp.down_proj": {"storage_bits": 1, "bits": 1}})
+
+    blk = jnn.SparseMoeBlock(H, I, E, K_TOP, shared_hidden=256, group_size=64, bits=2,
+                             router_bits=8, shared_bits=8, device="cuda")
+    rep = loader.load_bundle_into(blk, tmp_path)
+    assert rep.expanded == ["switch_mlp.down_proj"] and not rep.missing and not rep.unexpected
+    two = O.expand_1bit_to_2bit(one)
+    dn = blk.switch_mlp.down_proj
+    assert (dn.bits, dn.group_size) == (2, 128)
+    np.testing.assert_array_equal(dn.weight.cpu().numpy().view(np.uint32), two)
+
+    x = O.round_bf16(np.random.default_rng(12).standard_normal((3, H), dtype=np.float32))
+    y = blk(to_tensor(x, "bf16"))
+    f = lambda name: (q[name][0], O.sidecar_f32(q[name][1], "bf16"),
+                      O.sidecar_f32(q[name][2], "bf16"))
+    gp, gs_, gb = f("gate")
+    logits = O.round_bf16(O.quantized_matmul(x, gp, gs_, gb, 8, 64))
+    idx, sc = O.route_topk(logits, K_TOP)
+    # each pair in the stock order and roundings (g, u, h and the expert output in bf16)
+    outs = []
+    for t_ in range(x.shape[0]):
+        rows = []
+        for j in range(K_TOP):
+            e = idx[t_, j]
+            g = O.round_bf16(O.quantized_matmul(x[t_:t_ + 1], q["switch_mlp.gate_proj"][0][e],
+                                                O.sidecar_f32(q["switch_mlp.gate_proj"][1][e], "bf16"),
+                                                O.sidecar_f32(q["switch_mlp.gate_proj"][2][e], "bf16"), 3, 128))
+            u = O.round_bf16(O.quantized_matmul(x[t_:t_ + 1], q["switch_mlp.up_proj"][0][e],
+                                                O.sidecar_f32(q["switch_mlp.up_proj"][1][e], "bf16"),
+                                                O.sidecar_f32(q["switch_mlp.up_proj"][2][e], "bf16"), 3, 128))
+            h = O.round_bf16(O.silu(g) * u.astype(np.float64))
+            rows.append(O.round_bf16(O.quantized_matmul(h, two[e], O.sidecar_f32(ds[e], "bf16"),
+                                                        O.sidecar_f32(db[e], "bf16"), 2, 128))[0])
+        outs.append(np.stack(rows))
+    sw = np.stack(outs)
+    routed = O.round_bf16((sw.astype(np.float64) * sc[..., None]).sum(1))
+    sg, su, sd = f("shared_expert.gate_proj"), f("shared_expert.up_proj"), f("shared_expert.down_proj")
+    g = O.round_bf16(O.quantized_matmul(x, *sg, 8, 64))
+    u = O.round_bf16(O.quantized_matmul(x, *su, 8, 64))
+    h = O.round_bf16(O.silu(g) * u)
+    shared = O.round_bf16(O.quantized_matmul(h, *sd, 8, 64))
+    assert_close(values_of(y), O.round_bf16(routed + shared), "loaded moe block")

@@ -248,39 +248,41 @@ def test_switch_glu_direct_pairs(T, k, E):
     assert_close(values_of(y).reshape(T * k, 1, I), O.round_bf16(refg), "gather direct")
 
 
-@pytest.mark.parametrize("T,k,E,H,I,bits_d,gs,with_shared", [
-    (1, 4, 128, 512, 256, 2, 64, True),     # config-3 shape class: combine inside the down launch
-    (1, 10, 512, 512, 256, 2, 128, True),   # config-5 routing: top-10 of 512
-    (2, 8, 64, 256, 384, 4, 64, False),
-    (3, 2, 16, 384, 128, 3, 64, True),      # 32-lane rows (two rows per wave instruction)
-    (1, 4, 4, 4096, 2048, 2, 64, True),     # config-3 sizes (LDS staging of 4 x 2048 rows)
-    (64, 4, 128, 512, 256, 2, 64, True),    # above decode sizes: the two-call form
+@pytest.mark.parametrize("T,k,E,H,I,bits_d,gs,with_shared,xdt", [
+    (1, 4, 128, 512, 256, 2, 64, True, "bf16"),    # config-3 shape class: combine inside the down launch
+    (1, 10, 512, 512, 256, 2, 128, True, "bf16"),  # config-5 routing: top-10 of 512
+    (2, 8, 64, 256, 384, 4, 64, False, "bf16"),
+    (3, 2, 16, 384, 128, 3, 64, True, "bf16"),     # 32-lane rows (two rows per wave instruction)
+    (1, 4, 4, 4096, 2048, 2, 64, True, "bf16"),    # config-3 sizes (down rows of 2048)
+    (1, 6, 32, 256, 256, 8, 32, True, "f16"),      # f16, 8-bit down, group 32
+    (2, 4, 16, 256, 512, 6, 64, False, "f16"),     # f16, 6-bit down
+    (64, 4, 128, 512, 256, 2, 64, True, "bf16"),   # above decode sizes: the two-call form
 ])
-def test_switch_glu_combine(T, k, E, H, I, bits_d, gs, with_shared):
+def test_switch_glu_combine(T, k, E, H, I, bits_d, gs, with_shared, xdt):
     """Routed experts plus combine in one call: bit-identical to switch_glu followed by
     moe_combine on the GPU, and within tolerance of the oracle's composition."""
-    g = _stack(E, I, H, 2, gs, seed=41)
-    u = _stack(E, I, H, 2, gs, seed=42)
-    d = _stack(E, H, I, bits_d, gs, seed=43)
+    g = QWeight(I, H, 2, gs, seed=41, experts=E, sidecar=xdt)
+    u = QWeight(I, H, 2, gs, seed=42, experts=E, sidecar=xdt)
+    d = QWeight(H, I, bits_d, gs, seed=43, experts=E, sidecar=xdt)
     rng = np.random.default_rng(T * 7 + k)
-    x = O.round_bf16(rng.standard_normal((T, H), dtype=np.float32))
+    x = O.round_to(rng.standard_normal((T, H), dtype=np.float32), xdt)
     inds = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
     w = rng.random((T, k)).astype(np.float32)
-    sh = O.round_bf16(rng.standard_normal((T, H), dtype=np.float32))
-    tx, ti, tw = to_tensor(x, "bf16"), torch.from_numpy(inds).cuda(), torch.from_numpy(w).cuda()
-    tsh = to_tensor(sh, "bf16") if with_shared else None
+    sh = O.round_to(rng.standard_normal((T, H), dtype=np.float32), xdt)
+    tx, ti, tw = to_tensor(x, xdt), torch.from_numpy(inds).cuda(), torch.from_numpy(w).cuda()
+    tsh = to_tensor(sh, xdt) if with_shared else None
     gt, ut, dt_ = (g.dw, g.ds, g.db, 2), (u.dw, u.ds, u.db, 2), (d.dw, d.ds, d.db, bits_d)
     got = jq.switch_glu_combine(tx, ti, tw, gt, ut, dt_, gs, tsh)
     two = jq.moe_combine(jq.switch_glu(tx, ti, gt, ut, dt_, gs), tw, tsh)
     assert tuple(got.shape) == (T, H)
     assert torch.equal(got.view(torch.int16), two.view(torch.int16)), "fused != two calls"
     sw, _ = O.switch_glu(x, inds, (g.packed, g.s, g.b, 2), (u.packed, u.s, u.b, 2),
-                         (d.packed, d.s, d.b, bits_d), gs, "bf16")
-    ref = O.moe_combine(sw, w, sh if with_shared else None, "bf16")
+                         (d.packed, d.s, d.b, bits_d), gs, xdt)
+    ref = O.moe_combine(sw, w, sh if with_shared else None, xdt)
     # The value before the last rounding (slot sum rounded, + shared): the max-abs bound then
-    # charges only what lies beyond the final bf16 rounding.
+    # charges only what lies beyond the final rounding.
     pre = (sw.astype(np.float64) * w[..., None]).sum(1)
     if with_shared:
-        pre = O.round_bf16(pre).astype(np.float64) + sh
-    assert_close(values_of(got), ref, f"switch_glu_combine T{T} k{k} E{E}", exact=pre,
-                 out_dtype="bf16")
+        pre = O.round_to(pre, xdt).astype(np.float64) + sh
+    assert_close(values_of(got), ref, f"switch_glu_combine T{T} k{k} E{E} {xdt}", exact=pre,
+                 out_dtype=xdt)
