@@ -142,6 +142,25 @@ int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
                               jq_stream_t stream);
 
 /*
+ * OCP MX modes as MLX stores them (mode "mxfp4" = 4, "mxfp8" = 8; group size 32, no biases):
+ *   W[n, k] = value(code[n, k]) * 2^(scales[n, k/32] - 127)
+ *   codes   uint32 [rows, K*mode/32], little-endian bytes: mxfp4 two E2M1 codes per byte
+ *           (element 2i in the low nibble), mxfp8 one E4M3 (FN) byte per element
+ *   scales  uint8 [rows, K/32] E8M0 exponents (255 = NaN)
+ * jq_mx_dequantize writes W (out_dtype; exact in fp32). jq_mx_quantized_matmul computes
+ * y[M, N] = x[M, K] @ W^T (x bf16/f16, fp32 accumulation, K <= 16384) as decode GEMVs, one
+ * launch per activation row. Replace mx.dequantize / mx.quantized_matmul with mode
+ * "mxfp4"/"mxfp8", the modes the loader switches a module to when its scales are uint8
+ * (jang-tools/jang_tools/loader.py:1877-1912); format per
+ * jang-tools/jang_tools/mimo_v2/mxfp4_codec.py:1-50.
+ */
+int jq_mx_dequantize(const uint32_t* codes, const uint8_t* scales, int mode, int64_t rows,
+                     int64_t K, void* out, int out_dtype, jq_stream_t stream);
+int jq_mx_quantized_matmul(const void* x, int x_dtype, const uint32_t* codes,
+                           const uint8_t* scales, int mode, int64_t M, int64_t N, int64_t K,
+                           void* y, int y_dtype, jq_stream_t stream);
+
+/*
  * Router: probs = softmax(logits) in fp32 (max-subtracted, "precise"), top-k expert ids
  * per token (ties -> lower id first), weights = their probabilities, optionally divided
  * by their sum (norm_topk_prob). logits f32 [T, E]; idx uint32 [T, k]; weights f32 [T, k].

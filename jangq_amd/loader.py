@@ -12,8 +12,9 @@ torch modules on the GPU:
     (affine.py:466-545); here the expansion runs on the GPU (``jq_expand_1bit_to_2bit``);
   - every quantized module's bits and group size are then fixed from its tensor shapes
     (``_fix_quantized_bits``, loader.py:1851-1982, through :func:`shapes.infer_bits_group_size`).
-MXFP4 / MXFP8 modules (uint8 UE8M0 scales, loader.py:1877-1912) are not on this build's path
-and raise.
+A dense module whose scales are uint8 (E8M0) switches to the MX mode its shapes give, mxfp4
+or mxfp8 at group size 32, and drops the affine biases (loader.py:1877-1912); expert stacks
+in an MX mode raise (the gathered launches are affine only).
 """
 from __future__ import annotations
 
@@ -35,8 +36,9 @@ _QUANT_ATTRS = ("weight", "scales", "biases")
 @dataclass
 class LoadReport:
     """What a load did: tensors assigned, modules whose bits / group size changed
-    ({path: (bits, group_size)}), modules expanded from 1-bit storage, and the bundle keys
-    that matched nothing / module tensors the bundle did not hold."""
+    ({path: (bits, group_size)}, or (mode, bits, 32) for an MX mode), modules expanded from
+    1-bit storage, and the bundle keys that matched nothing / module tensors the bundle did
+    not hold."""
     loaded: int = 0
     fixed: dict = field(default_factory=dict)
     expanded: list = field(default_factory=list)
@@ -97,6 +99,31 @@ def _fix_bits(path: str, module, w_cols: int, s_cols: int) -> tuple[int, int]:
                                  logical_in=logical_in, is_router=is_router_name(path))
 
 
+def _load_mx(mod: str, m, w: torch.Tensor, s: torch.Tensor, device, report: LoadReport):
+    """uint8 E8M0 scales: mxfp4 when 32 * scale columns == 8 * word columns, mxfp8 when
+    == 4 * word columns (loader.py:1877-1912); no biases."""
+    if isinstance(m, jnn.QuantizedSwitchLinear):
+        raise NotImplementedError(f"{mod}: MX-mode expert stacks are not implemented "
+                                  "(the gathered launches are affine only)")
+    w_cols, s_cols = w.shape[-1], s.shape[-1]
+    if s_cols * 32 == w_cols * 8:
+        mode, bits = "mxfp4", 4
+    elif s_cols * 32 == w_cols * 4:
+        mode, bits = "mxfp8", 8
+    else:
+        raise ValueError(f"{mod}: uint8 scales {tuple(s.shape)} fit no MX mode for weight "
+                         f"{tuple(w.shape)}")
+    if s_cols * 32 != m.in_features or tuple(w.shape[:-1]) != tuple(m.weight.shape[:-1]):
+        raise ValueError(f"{mod}: {mode} shapes {tuple(w.shape)} / {tuple(s.shape)} do not fit "
+                         f"the module ({m.out_features} x {m.in_features})")
+    m.weight = w.view(torch.int32).to(device)
+    m.scales = s.to(device)
+    m.biases = None
+    m.bits, m.group_size, m.mode = bits, 32, mode
+    report.fixed[mod] = (mode, bits, 32)
+    report.loaded += 2
+
+
 def load_bundle_into(model: torch.nn.Module, path, *, device=None,
                      strict: bool = False) -> LoadReport:
     """Assign a v2 bundle's tensors to ``model``'s quantized modules (QuantizedLinear,
@@ -139,14 +166,15 @@ def load_bundle_into(model: torch.nn.Module, path, *, device=None,
 
     for mod, tensors in pending.items():
         m = quant[mod]
-        lacking = [a for a in _QUANT_ATTRS if a not in tensors]
+        mx = "scales" in tensors and tensors["scales"].dtype == torch.uint8
+        lacking = [a for a in _QUANT_ATTRS if a not in tensors and not (mx and a == "biases")]
         if lacking:
             report.missing += [f"{mod}.{a}" for a in lacking]
             continue
+        if mx:
+            _load_mx(mod, m, tensors["weight"], tensors["scales"], device, report)
+            continue
         w, s, b = tensors["weight"], tensors["scales"], tensors["biases"]
-        if s.dtype == torch.uint8:
-            raise NotImplementedError(f"{mod}: uint8 (UE8M0) scales are the MXFP4/MXFP8 modes, "
-                                      "which this build does not run")
         if w.dtype not in (torch.uint32, torch.int32):
             raise ValueError(f"{mod}.weight: packed codes must be uint32 words, got {w.dtype}")
         if s.dtype not in (torch.bfloat16, torch.float16, torch.float32) or b.dtype != s.dtype:

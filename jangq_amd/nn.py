@@ -47,7 +47,7 @@ class QuantizedLinear(torch.nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         y = ops.quantized_matmul(x, self.weight, self.scales, self.biases, True,
-                                 self.group_size, self.bits)
+                                 self.group_size, self.bits, self.mode)
         return y if self.bias is None else y + self.bias
 
 

@@ -57,9 +57,12 @@ def _codes(w: torch.Tensor) -> torch.Tensor:
     return _dev(w, "packed weight")
 
 
+MX_MODES = {"mxfp4": 4, "mxfp8": 8}
+
+
 def _check_mode(mode: str, transpose: bool) -> None:
-    if mode != "affine":
-        raise ValueError(f"mode={mode!r}: only the affine mode is implemented")
+    if mode != "affine" and mode not in MX_MODES:
+        raise ValueError(f"mode={mode!r}: the modes are affine, mxfp4 and mxfp8")
     if not transpose:
         raise ValueError("transpose=False is not supported (every reference call uses transpose=True)")
 
@@ -97,6 +100,8 @@ def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
     """W = q*scale + bias per group, fp32 arithmetic, returned as ``dtype`` (default
     scales.dtype, as mx.dequantize). 2-D or stacked [E, N, P] weights."""
     _check_mode(mode, True)
+    if mode in MX_MODES:
+        return _mx_dequantize(w, scales, group_size, bits, mode, dtype or torch.bfloat16)
     _check_bits_gs(bits, group_size)
     w = _codes(w)
     scales = _dev(scales, "scales")
@@ -140,12 +145,52 @@ def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4, mode: str = "
     return wq.view(torch.uint32), scales, biases
 
 
+def _mx_check(w, scales, group_size, bits, mode):
+    if group_size != 32 or bits != MX_MODES[mode]:
+        raise ValueError(f"mode={mode!r} needs group_size=32 and bits={MX_MODES[mode]}")
+    w = _codes(w)
+    scales = _dev(scales, "scales")
+    if scales.dtype != torch.uint8:
+        raise ValueError(f"{mode} scales are uint8 E8M0 exponents, got {scales.dtype}")
+    K = w.shape[-1] * 32 // bits
+    if tuple(scales.shape) != (*w.shape[:-1], K // 32):
+        raise ValueError(f"scales must be {(*w.shape[:-1], K // 32)}, got {tuple(scales.shape)}")
+    return w, scales, K
+
+
+def _mx_dequantize(w, scales, group_size, bits, mode, dtype):
+    """mx.dequantize for the MX modes: value(code) * 2^(scale - 127), exact in fp32."""
+    w, scales, K = _mx_check(w, scales, group_size, bits, mode)
+    out = torch.empty((*w.shape[:-1], K), dtype=dtype, device=w.device)
+    _lib.check(_lib.lib().jq_mx_dequantize(_ptr(w), _ptr(scales), bits, math.prod(w.shape[:-1]),
+                                           K, _ptr(out), _dtype_code(out, "output"), _stream()),
+               "dequantize")
+    return out
+
+
+def _mx_matmul(x, w, scales, group_size, bits, mode, out):
+    """mx.quantized_matmul for the MX modes (no biases): decode GEMVs, one per activation row."""
+    w, scales, K = _mx_check(w, scales, group_size, bits, mode)
+    x = _dev(x, "x")
+    if w.dim() != 2 or x.shape[-1] != K:
+        raise ValueError(f"x last dim {x.shape[-1]} / w {tuple(w.shape)} do not match K {K}")
+    N, M = w.shape[0], math.prod(x.shape[:-1])
+    if out is None:
+        out = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().jq_mx_quantized_matmul(
+        _ptr(x), _dtype_code(x, "x"), _ptr(w), _ptr(scales), bits, M, N, K, _ptr(out),
+        _dtype_code(out, "output"), _stream()), "quantized_matmul")
+    return out
+
+
 def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                      biases: torch.Tensor, transpose: bool = True, group_size: int = 64,
                      bits: int = 4, mode: str = "affine", *,
                      out: torch.Tensor | None = None) -> torch.Tensor:
     """y = x @ dequantize(w)^T with fp32 accumulation; y has x's dtype and shape [..., N]."""
     _check_mode(mode, transpose)
+    if mode in MX_MODES:
+        return _mx_matmul(x, w, scales, group_size, bits, mode, out)
     _check_bits_gs(bits, group_size)
     if biases is None:
         raise ValueError("affine mode needs biases")
@@ -233,6 +278,8 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     entry, broadcast against rhs); rhs indexes experts (default: arange(E)).
     Output [*broadcast(lhs, rhs), M, N] in x.dtype."""
     _check_mode(mode, transpose)
+    if mode in MX_MODES:
+        raise ValueError(f"gather_qmm: mode={mode!r} is not implemented (affine only)")
     _check_bits_gs(bits, group_size)
     if biases is None:
         raise ValueError("affine mode needs biases")

@@ -16,6 +16,11 @@ checkout) in numpy:
   gather_qmm                   naive per-pair loop of jang_tools/dots3/ops_selftest.py:18-28
   switch_glu                   mlx_lm SwitchGLU as restated at dots3/ops.py:195-223
   route_topk                   qwen4_exp/modeling.py:587-593
+  mx_dequantize                OCP MX modes as MLX stores them: mxfp4 per
+                               jang-tools/jang_tools/mimo_v2/mxfp4_codec.py:1-50 (E2M1 nibbles,
+                               low nibble = even element, E8M0 block scales, 32 per block, the
+                               bytes read as little-endian uint32 words); mxfp8 the same with
+                               one E4M3 byte per element (loader.py:1877-1912 mode switch)
 
 How each is pinned (tests/test_oracle.py):
   pack/unpack       known answers of jang-tools/tests/test_pack.py:33-61, the LSB-first 3-bit
@@ -297,6 +302,57 @@ def route_topk(logits, k: int, renorm: bool = True):
     if renorm:
         w = w / w.sum(axis=-1, keepdims=True)
     return idx.astype(np.int64), w
+
+
+# ----------------------------------------------------------------------------- MX modes
+
+MX_BLOCK = 32
+# E2M1 magnitudes of codes 0..7 (mxfp4_codec.py:22-26); code | 8 is the negative.
+E2M1_TABLE = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+                       -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0], dtype=np.float32)
+
+
+def e4m3_to_f32(b) -> np.ndarray:
+    """OCP E4M3 (FN: bias 7, no infinities, S.1111.111 = NaN) bytes to fp32."""
+    b = np.asarray(b, dtype=np.uint8).astype(np.int64)
+    sgn = np.where(b & 0x80, -1.0, 1.0)
+    e, m = (b >> 3) & 15, b & 7
+    mag = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    out = sgn * mag
+    return np.where((e == 15) & (m == 7), np.nan, out).astype(np.float32)
+
+
+def e8m0_to_f32(e) -> np.ndarray:
+    """E8M0 block scale: 2^(e - 127); 255 is NaN."""
+    e = np.asarray(e, dtype=np.uint8).astype(np.float64)
+    return np.where(e == 255, np.nan, np.exp2(e - 127.0)).astype(np.float32)
+
+
+def mx_codes(packed, mode: str) -> np.ndarray:
+    """Element codes of MX rows [rows, P] (uint32): 8 nibbles per word (mxfp4, element 2i in
+    the low nibble of byte i) or 4 bytes per word (mxfp8), little-endian."""
+    by = np.ascontiguousarray(np.asarray(packed, dtype=np.uint32)).view(np.uint8)
+    by = by.reshape(*np.asarray(packed).shape[:-1], -1)
+    if mode == "mxfp4":
+        return np.stack([by & 15, by >> 4], axis=-1).reshape(*by.shape[:-1], -1)
+    if mode == "mxfp8":
+        return by
+    raise ValueError(mode)
+
+
+def mx_dequantize(packed, scales_u8, mode: str) -> np.ndarray:
+    """W[n, k] = value(code[n, k]) * 2^(scale[n, k // 32] - 127) in fp32 (exact: a small
+    float times a power of two)."""
+    c = mx_codes(packed, mode)
+    v = E2M1_TABLE[c] if mode == "mxfp4" else e4m3_to_f32(c)
+    s = e8m0_to_f32(scales_u8)
+    return (v.reshape(*c.shape[:-1], -1, MX_BLOCK) * s[..., None]).reshape(c.shape)
+
+
+def mx_quantized_matmul(x_f32, packed, scales_u8, mode: str) -> np.ndarray:
+    """y = x @ mx_dequantize(W)^T accumulated in fp64."""
+    W = mx_dequantize(packed, scales_u8, mode).astype(np.float64)
+    return np.asarray(x_f32, dtype=np.float64) @ W.T
 
 
 # ----------------------------------------------------------------------------- metrics

@@ -54,8 +54,10 @@ def test_operator_argument_checks_run_before_launch():
         ops.quantized_matmul(x, w, s, s, group_size=48)
     with pytest.raises(ValueError, match="transpose"):
         ops.quantized_matmul(x, w, s, s, transpose=False)
-    with pytest.raises(ValueError, match="affine"):
-        ops.quantized_matmul(x, w, s, s, mode="mxfp4")
+    with pytest.raises(ValueError, match="affine, mxfp4 and mxfp8"):
+        ops.quantized_matmul(x, w, s, s, mode="nvfp4")
+    with pytest.raises(ValueError, match="group_size=32"):
+        ops.quantized_matmul(x, w, s, s, mode="mxfp4")  # MX modes are group 32, bits 4 / 8
     with pytest.raises(ValueError, match="GPU"):
         ops.quantized_matmul(x, w, s, s)  # CPU tensors are refused: no CPU fallback
 

@@ -89,12 +89,31 @@ def test_format_checks(tmp_path):
         loader.load_bundle_into(_block(), tmp_path / "d")
 
 
-def test_mxfp_scales_refused(tmp_path):
+def test_mx_scales_switch_the_mode(tmp_path):
+    """uint8 scales: mxfp4 / mxfp8 chosen from the shapes, biases dropped (loader.py:1877-1912);
+    MX expert stacks are refused."""
+    rng = np.random.default_rng(4)
     t = _bundle_tensors()
-    t["gate.scales"] = torch.zeros_like(t["gate.scales"], dtype=torch.uint8)
+    # router as mxfp8 (4 elements per word), shared down as mxfp4 (8 per word)
+    t["gate.weight"] = torch.from_numpy(
+        rng.integers(0, 2**32, (E, H // 4), dtype=np.uint64).astype(np.uint32).view(np.int32)).view(torch.uint32)
+    t["gate.scales"] = torch.full((E, H // 32), 120, dtype=torch.uint8)
+    del t["gate.biases"]
+    t["shared_expert.down_proj.weight"] = torch.from_numpy(
+        rng.integers(0, 2**32, (H, 256 // 8), dtype=np.uint64).astype(np.uint32).view(np.int32)).view(torch.uint32)
+    t["shared_expert.down_proj.scales"] = torch.full((H, 256 // 32), 127, dtype=torch.uint8)
     write_bundle(tmp_path, t)
-    with pytest.raises(NotImplementedError, match="MXFP"):
-        loader.load_bundle_into(_block(), tmp_path)
+    blk = _block()
+    rep = loader.load_bundle_into(blk, tmp_path)
+    assert rep.fixed["gate"] == ("mxfp8", 8, 32)
+    assert rep.fixed["shared_expert.down_proj"] == ("mxfp4", 4, 32)
+    assert blk.gate.mode == "mxfp8" and blk.gate.biases is None
+    assert blk.shared_expert.down_proj.mode == "mxfp4"
+    t["switch_mlp.down_proj.scales"] = torch.zeros((E, H, I // 32), dtype=torch.uint8)
+    t["switch_mlp.down_proj.weight"] = torch.zeros((E, H, I // 8), dtype=torch.uint32)
+    write_bundle(tmp_path / "x", t)
+    with pytest.raises(NotImplementedError, match="MX-mode expert"):
+        loader.load_bundle_into(_block(), tmp_path / "x")
 
 
 def test_shapes_that_fit_nothing(tmp_path):

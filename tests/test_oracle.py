@@ -17,6 +17,7 @@ from pathlib import Path
 
 import numpy as np
 import pytest
+import torch
 
 from oracle import jangq_oracle as O
 
@@ -406,3 +407,60 @@ def test_dequantize_tensor_flat_vs_loop_and_row_layout(bits):
     rows = O.dequantize_affine(q.view(np.uint32).reshape(n_blocks, bs * bits // 32),
                                s.astype(np.float32)[:, None], b.astype(np.float32)[:, None], bits, bs)
     np.testing.assert_array_equal(got.reshape(-1), rows.reshape(-1)[:150])
+
+
+# ----------------------------------------------------------------------------- MX modes
+
+
+def test_e2m1_table_matches_the_format():
+    """The restated mxfp4 value table against the E2M1 definition (1 sign, 2 exponent bits with
+    bias 1, 1 mantissa bit; exponent 0 is subnormal)."""
+    for c in range(16):
+        sgn = -1.0 if c & 8 else 1.0
+        e, m = (c >> 1) & 3, c & 1
+        mag = m * 0.5 if e == 0 else 2.0 ** (e - 1) * (1 + m / 2)
+        assert O.E2M1_TABLE[c] == sgn * mag and np.signbit(O.E2M1_TABLE[c]) == bool(c & 8)
+
+
+def test_e4m3_and_e8m0_match_torch():
+    b = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(b).view(torch.float8_e4m3fn).float().numpy()
+    got = O.e4m3_to_f32(b)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    np.testing.assert_array_equal(got[~np.isnan(got)], ref[~np.isnan(ref)])
+    ref8 = torch.from_numpy(b).view(torch.float8_e8m0fnu).float().numpy()
+    got8 = O.e8m0_to_f32(b)
+    np.testing.assert_array_equal(np.isnan(got8), np.isnan(ref8))
+    np.testing.assert_array_equal(got8[:255], ref8[:255])
+
+
+def test_mx_layout_and_brute_force():
+    """Element 2i sits in the low nibble of byte i (mxfp4_codec.py:8), bytes little-endian in
+    the uint32 words; scales one per 32 elements. Checked against a pure-Python loop."""
+    w = np.array([[0x00000021]], dtype=np.uint32)  # bytes 21 00 00 00
+    np.testing.assert_array_equal(O.mx_codes(w, "mxfp4")[0, :4], [1, 2, 0, 0])
+    np.testing.assert_array_equal(O.mx_codes(w, "mxfp8")[0], [0x21, 0, 0, 0])
+    rng = np.random.default_rng(3)
+    for mode, per_word in (("mxfp4", 8), ("mxfp8", 4)):
+        K = 64
+        packed = rng.integers(0, 2**32, (3, K // per_word), dtype=np.uint64).astype(np.uint32)
+        if mode == "mxfp8":  # no NaN codes (S.1111.111)
+            by = packed.view(np.uint8)
+            by[(by & 0x7F) == 0x7F] = 0x7E
+        sc = rng.integers(100, 140, (3, K // 32)).astype(np.uint8)
+        got = O.mx_dequantize(packed, sc, mode)
+        for r in range(3):
+            word_bytes = [int(x) for x in packed[r].view(np.uint8)]
+            for k in range(K):
+                if mode == "mxfp4":
+                    byte = word_bytes[k // 2]
+                    code = (byte >> 4) if k % 2 else (byte & 15)
+                    sgn = -1.0 if code & 8 else 1.0
+                    e, m = (code >> 1) & 3, code & 1
+                    v = sgn * (m * 0.5 if e == 0 else 2.0 ** (e - 1) * (1 + m / 2))
+                else:
+                    byte = word_bytes[k]
+                    sgn = -1.0 if byte & 0x80 else 1.0
+                    e, m = (byte >> 3) & 15, byte & 7
+                    v = sgn * (m * 2.0 ** -9 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7))
+                assert got[r, k] == np.float32(v * 2.0 ** (int(sc[r, k // 32]) - 127)), (mode, r, k)
