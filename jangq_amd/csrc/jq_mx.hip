@@ -15,8 +15,10 @@
 //
 // GEMV: a wave owns rows, a lane owns the row's 32-element blocks l, l + 64, ...; the lane's
 // activations of those blocks stay in registers (as bf16/f16 pairs) while the wave walks its
-// rows. Per block: decode, multiply-add in fp32, times the block scale; a DPP wave sum ends a
-// row. Activation rows are taken one launch each (decode batches).
+// rows. Per block: the gfx950 MX conversions turn each code pair into a bf16/f16 pair of the
+// activations' type (unscaled: E2M1 and E4M3 values are exact in both), v_dot2 accumulates in
+// fp32, and the block scale multiplies the block's sum; a DPP wave sum ends a row. Activation
+// rows are taken one launch each (decode batches).
 #include <math.h>
 
 #include "jq_common.h"
@@ -69,15 +71,30 @@ __global__ void __launch_bounds__(256) mx_dequant_kernel(const uint32_t* __restr
   }
 }
 
-// Activation element pair (2i, 2i + 1) of a bf16/f16 row as fp32.
-template <int XD>
-JQ_DEV void x_pair(uint32_t p, float& a, float& b) {
-  if constexpr (XD == JQ_BF16) {
-    a = __uint_as_float(p << 16);
-    b = __uint_as_float(p & 0xFFFF0000u);
+// Elements 2e, 2e + 1 of a block (code words w) as a pair of the activations' 16-bit type:
+// mxfp4 byte e % 4 of word e / 4, mxfp8 bytes 2 (e % 2), + 1 of word e / 2; the lower
+// element lands in the low half.
+template <int MODE, int XD, int E>
+JQ_DEV uint32_t mx_pair(const uint32_t* w) {
+  if constexpr (MODE == 4) {
+    if constexpr (XD == JQ_BF16)
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[E >> 2], 1.0f, E & 3));
+    else
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w[E >> 2], 1.0f, E & 3));
   } else {
-    a = f16_bits_to_f32((uint16_t)(p & 0xFFFFu));
-    b = f16_bits_to_f32((uint16_t)(p >> 16));
+    if constexpr (XD == JQ_BF16)
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[E >> 1], 1.0f, (E & 1) != 0));
+    else
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[E >> 1], 1.0f, (E & 1) != 0));
+  }
+}
+
+template <int MODE, int XD, int E = 0>
+JQ_DEV float block_dot(const uint32_t* w, const uint32_t* xp, float part) {
+  if constexpr (E == 16) {
+    return part;
+  } else {
+    return block_dot<MODE, XD, E + 1>(w, xp, dot2<XD>(mx_pair<MODE, XD, E>(w), xp[E], part));
   }
 }
 
@@ -127,18 +144,7 @@ __global__ void __launch_bounds__(256) mx_gemv_kernel(const uint16_t* __restrict
           w[4 * v] = t.x; w[4 * v + 1] = t.y; w[4 * v + 2] = t.z; w[4 * v + 3] = t.w;
         }
         const float s = e8m0_f32(srow[b]);
-        float part = 0.f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {  // element pair e = elements 2e, 2e + 1
-          float xa0, xa1;
-          x_pair<XD>(xa[q][e], xa0, xa1);
-          constexpr int PER = MODE == 4 ? 8 : 4;
-          const uint32_t word = w[(2 * e) / PER];
-          const int j = (2 * e) % PER;
-          part = fmaf(mx_value<MODE>(word, j), xa0, part);
-          part = fmaf(mx_value<MODE>(word, j + 1), xa1, part);
-        }
-        acc = fmaf(part, s, acc);
+        acc = fmaf(block_dot<MODE, XD>(w, xa[q], 0.f), s, acc);
       }
     }
     const float tot = jqg::wave_total_lane63(acc);
