@@ -9,6 +9,9 @@
 // one contiguous run of a row (buffer loads of 16 / 12 / 8 bytes per lane), and the lane's K
 // slice is the same for every row.
 //
+// For one activation row whose rows take at most two waves of chunks, gemv_row_kernel instead
+// gives each wave whole rows (a lane takes chunks l, l + 64): one DPP sum per row, no LDS.
+//
 // Activation-stationary and persistent. Blocks stay resident and walk row blocks b,
 // b + gridDim.x, ...; a lane loads its K slice of x once and keeps it in registers in the
 // pairing the code unpack produces, with two per-unit constants, X = sum x and
@@ -201,18 +204,157 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_kernel(GemvArgs a) {
   }
 }
 
-// Blocks of gemv_kernel<D, SB, MT, RB> (kw waves) the GPU holds at once.
-template <class D, int SB, int MT, int RB>
-int64_t resident_blocks(int kw) {
+// One activation row, whole rows per wave: lane l owns chunks l, l + 64, ... (CPL of them) of
+// every row, so a row's sum is one DPP wave reduction and no LDS or barrier is involved. The
+// waves (4 per block) are independent and persistent over row blocks of RB rows, with the
+// same rolling register ring as gemv_kernel.
+template <class D, int SB, int CPL, int RB>
+__global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a) {
+  constexpr int BITS = D::BITS;
+  constexpr int UPL = units_per_chunk<BITS>();
+  constexpr int NW = BITS * UPL;
+  const int total = a.rb_begin[a.nprob];
+  const int nwaves = (int)gridDim.x * 4;
+  int it = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+  if (it >= total) return;  // this wave (no block-wide synchronisation below)
+  const int K = a.b.K;
+  const int lane = threadIdx.x & 63;
+  const int C = K / (32 * UPL);
+  const uint32_t rowbytes = (uint32_t)(K / 32) * BITS * 4;
+  const uint32_t sbrow = (uint32_t)(K >> (a.ushift + 5)) * 2;
+  bool act[CPL];
+  uint32_t voff[CPL], vsb[CPL][UPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    act[j] = c < C;
+    const int ci = act[j] ? c : 0;
+    voff[j] = (uint32_t)ci * (4 * NW);
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) vsb[j][t] = (uint32_t)((ci * UPL + t) >> a.ushift) * 2;
+  }
+  jqd::XRaw xr[CPL][UPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+#pragma unroll
+    for (int t = 0; t < UPL; ++t)
+      jqd::load_xraw((const uint16_t*)a.b.p[0].x + (int64_t)(voff[j] / (4 * NW) * UPL + t) * 32,
+                     xr[j][t]);
+  auto locate = [&](int i, int& p, int64_t& row0) {
+    p = 0;
+#pragma unroll
+    for (int q = 1; q < jqk::kMaxProblems; ++q)
+      if (q < a.nprob && i >= a.rb_begin[q]) p = q;
+    row0 = (int64_t)(i - a.rb_begin[p]) * RB;
+  };
+  auto views = [&](int p, int64_t row0, bool live, Rsrc& rc, Rsrc& rs, Rsrc& rb) {
+    const QmvProblem& pb = a.b.p[p];
+    const int64_t left = pb.N - row0;
+    const uint32_t rows = live ? (uint32_t)(left < RB ? left : RB) : 0u;
+    rc = make_rsrc((const char*)pb.codes + row0 * rowbytes, rows * rowbytes);
+    rs = make_rsrc((const char*)pb.scales + row0 * sbrow, rows * sbrow);
+    rb = make_rsrc((const char*)pb.biases + row0 * sbrow, rows * sbrow);
+  };
+  auto load_row = [&](Rsrc rc, Rsrc rs, Rsrc rb, int r, RowSlot<NW, UPL> (&slot)[CPL]) {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      load_chunk<NW>(rc, voff[j] + r * rowbytes, slot[j].w);
+#pragma unroll
+      for (int t = 0; t < UPL; ++t) {
+        slot[j].s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs, vsb[j][t] + r * sbrow, 0, 0);
+        slot[j].b[t] = __builtin_amdgcn_raw_buffer_load_b16(rb, vsb[j][t] + r * sbrow, 0, 0);
+      }
+    }
+  };
+  int p;
+  int64_t row0;
+  locate(it, p, row0);
+  Rsrc rc, rs, rbv;
+  views(p, row0, true, rc, rs, rbv);
+  RowSlot<NW, UPL> ring[RB][CPL];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    load_row(rc, rs, rbv, r, ring[r]);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  XState xs[CPL][UPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) {
+      jqd::XRaw& r = xr[j][t];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) r.d[i] = act[j] ? r.d[i] : 0u;
+      make_xstate<D>(r, xs[j][t]);
+    }
+  const Bases<D> bs = jqd::make_bases<D>();
+  for (;;) {
+    const int nx = it + nwaves;
+    const bool more = nx < total;
+    int p2;
+    int64_t row02;
+    locate(more ? nx : it, p2, row02);
+    Rsrc rc2, rs2, rb2;
+    views(p2, row02, more, rc2, rs2, rb2);
+    float acc[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      acc[r] = 0.f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int t = 0; t < UPL; ++t) {
+          const float sv = sb_to_f32<SB>(ring[r][j].s[t]);
+          const float bv = sb_to_f32<SB>(ring[r][j].b[t]);
+          const float d = unit_dot<D>(ring[r][j].w + t * BITS, bs, xs[j][t]);
+          acc[r] = fmaf(sv, d + xs[j][t].O, fmaf(bv, xs[j][t].X, acc[r]));
+        }
+      asm volatile("" : "+v"(acc[r])::"memory");
+      load_row(rc2, rs2, rb2, r, ring[r]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const QmvProblem& pb = a.b.p[p];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const float v = wave_total_lane63(acc[r]);
+      const int64_t row = row0 + r;
+      if (lane == 63 && row < pb.N) {
+        if (a.yd == JQ_BF16) store_t<JQ_BF16>(pb.y, row, v);
+        else if (a.yd == JQ_F16) store_t<JQ_F16>(pb.y, row, v);
+        else store_t<JQ_F32>(pb.y, row, v);
+      }
+    }
+    if (!more) break;
+    it = nx;
+    p = p2;
+    row0 = row02;
+  }
+}
+
+template <class D, int SB, int CPL, int RB>
+int launch_row(GemvArgs& a, hipStream_t st) {
+  a.kwshift = 0;
+  int total = 0;
+  for (int i = 0; i < a.nprob; ++i) {
+    a.rb_begin[i] = total;
+    total += (int)((a.b.p[i].N + RB - 1) / RB);
+  }
+  for (int i = a.nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
+  if (total == 0) return JQ_OK;
   int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_kernel<D, SB, MT, RB>, 64 * kw, 0) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_row_kernel<D, SB, CPL, RB>, 256, 0) !=
           hipSuccess || nb < 1)
     nb = 1;
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
-  return (int64_t)nb * cus;
+  const int64_t cap = (int64_t)nb * cus * 4;  // waves
+  const int64_t iters = (total + cap - 1) / cap;
+  const int64_t waves = (total + iters - 1) / iters;
+  gemv_row_kernel<D, SB, CPL, RB><<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(a);
+  return jqh::launch_status();
 }
 
 // Grid: as many blocks as fit the GPU at once, but no more than there are row blocks, with
@@ -230,34 +372,36 @@ int launch_rb(GemvArgs& a, hipStream_t st) {
   }
   for (int i = a.nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
   if (total == 0) return JQ_OK;
-  const int64_t cap = resident_blocks<D, SB, MT, RB>(kw);
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_kernel<D, SB, MT, RB>, 64 * kw, 0) !=
+          hipSuccess || nb < 1)
+    nb = 1;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  const int64_t cap = (int64_t)nb * cus;
   const int64_t iters = (total + cap - 1) / cap;
   const int grid = (int)((total + iters - 1) / iters);
   gemv_kernel<D, SB, MT, RB><<<grid, 64 * kw, 0, st>>>(a);
   return jqh::launch_status();
 }
 
-// Rows per block (the ring depth). Measured on MI355X: short rows (one or two waves per
-// block) do best with 4 rows, long rows (four or more waves, e.g. a 14336-wide down
-// projection) with 16; M = 4 keeps 4 rows for registers (18 per unit and token go to x).
-// At 5 and 6 bits (lane chunks of 20 / 24 bytes, two loads per row) short rows whose 4-row
-// blocks would all be resident at once take 2 rows, so that each block walks two or more:
-// config-2 q|k|v (6144 x 4096, 6-bit) 8.0 -> 7.4 us, o (4096 x 4096) 6.01 -> 5.96 us. At
-// 4 bits the same change was slower (4096 x 4096: 5.4 -> 5.7 us), as for long outputs
-// (3-bit gate|up 14.2 -> 15.2 us).
+// Rows per block (the ring depth). Measured on MI355X: long rows (four or more waves, e.g. a
+// 14336-wide down projection) do best in gemv_kernel with 16 rows; M = 2, 4 take 4 rows
+// (registers: 18 per unit and token go to x). One activation row with rows of at most two
+// waves of chunks runs gemv_row_kernel (whole rows per wave, 2 rows in flight), measured
+// against gemv_kernel: 4096 x 4096 4-bit 5.48 -> 5.03 us, config-2 q|k|v (6-bit) 7.40 ->
+// 7.02 us, o 5.96 -> 5.83 us, gate|up (3-bit) 13.98 -> 13.69 us; with 4 or 8 rows in flight
+// it was slower, and so were long rows (the down projection 9.12 -> 10.54 us).
 template <class D, int SB>
 int launch_m(GemvArgs& a, hipStream_t st) {
   constexpr bool two = D::BITS == 2;  // two units per lane chunk
-  const bool long_rows = gemv_waves(a.b.K, D::BITS, nullptr) >= 4;
+  const int kw = gemv_waves(a.b.K, D::BITS, nullptr);
   if (a.b.M == 1) {
-    if (long_rows) return launch_rb<D, SB, 1, 16>(a, st);
-    if constexpr (D::BITS == 5 || D::BITS == 6) {
-      int64_t rows = 0;
-      for (int i = 0; i < a.nprob; ++i) rows += a.b.p[i].N;
-      if ((rows + 3) / 4 <= resident_blocks<D, SB, 1, 4>(gemv_waves(a.b.K, D::BITS, nullptr)))
-        return launch_rb<D, SB, 1, 2>(a, st);
-    }
-    return launch_rb<D, SB, 1, 4>(a, st);
+    if (kw >= 4) return launch_rb<D, SB, 1, 16>(a, st);
+    if (kw == 1) return launch_row<D, SB, 1, 2>(a, st);
+    return launch_row<D, SB, 2, 2>(a, st);
   }
   if (a.b.M == 2) return launch_rb<D, SB, 2, 4>(a, st);
   if constexpr (!two) return launch_rb<D, SB, 4, 4>(a, st);
