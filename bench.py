@@ -442,7 +442,7 @@ def main():
             "parallelism": "single GPU",
         },
         "roofline": {
-            "kernel": "gemv_kernel, gate|up grouped launch (3-bit g64, 2 x 14336 x 4096, batch 1)",
+            "kernel": "gemv_row_kernel, gate|up grouped launch (3-bit g64, 2 x 14336 x 4096, batch 1)",
             "bound": "hbm",
             "achieved": round(res["gu_gbs"], 2),
             "peak": HBM_PEAK_GBS,
