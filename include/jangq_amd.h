@@ -259,6 +259,24 @@ int jq_switch_glu_combine(const void* x, int x_dtype, int64_t T, int64_t H, int6
                           void* workspace, int64_t workspace_bytes, jq_stream_t stream);
 
 /*
+ * Routing plus the routed experts of a MoE block: jq_moe_route(logits -> idx, weights), then
+ * jq_switch_glu_combine with them; idx uint32 [T, k] and weights f32 [T, k] are outputs (the
+ * same values jq_moe_route writes), logits f32 [T, E]. At decode sizes (E <= 512) the gate|up
+ * launch computes each token's top-k itself, so routing, gate|up and down+combine take two
+ * launches instead of three.
+ * Replaces qwen4_exp/modeling.py:587-597 after the router GEMV (jang-tools/jang_tools), the
+ * dispatches of dsv41/metal_decode.py:334-503.
+ */
+int jq_moe_experts(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E,
+                   const float* logits, int k, int renorm, uint32_t* idx, float* weights,
+                   const uint32_t* gate_codes, const void* gate_scales, const void* gate_biases,
+                   const uint32_t* up_codes, const void* up_scales, const void* up_biases,
+                   int bits_gu, const uint32_t* down_codes, const void* down_scales,
+                   const void* down_biases, int bits_d, int sb_dtype, int group_size,
+                   void* h_buf, void* y_buf, const void* shared, void* out, int y_dtype,
+                   void* workspace, int64_t workspace_bytes, jq_stream_t stream);
+
+/*
  * SwiGLU projection pair of a dense MLP: h = silu(round(x @ Wg^T)) * round(x @ Wu^T), each
  * product rounded to y_dtype first (as two quantized_matmul calls returning y_dtype give),
  * h rounded to y_dtype. Gate and up share bits, group size, N and K.

@@ -11,6 +11,7 @@ from .ops import (  # noqa: F401
     expand_packed_1bit_to_2bit,
     gather_qmm,
     moe_combine,
+    moe_experts,
     moe_route,
     quantize,
     quantized_matmul,
@@ -24,7 +25,7 @@ from ._lib import JangqError  # noqa: F401
 from .shapes import bit_inference, infer_bits_group_size  # noqa: F401
 
 __all__ = [
-    "dequantize", "dequantize_tensor", "expand_packed_1bit_to_2bit", "gather_qmm", "moe_combine", "moe_route", "quantize", "quantized_matmul",
+    "dequantize", "dequantize_tensor", "expand_packed_1bit_to_2bit", "gather_qmm", "moe_combine", "moe_experts", "moe_route", "quantize", "quantized_matmul",
     "quantized_matmul_multi", "quantized_swiglu", "switch_glu", "switch_glu_combine", "unpack", "bit_inference", "infer_bits_group_size",
     "JangqError",
 ]

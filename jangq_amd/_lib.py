@@ -49,6 +49,12 @@ SIGNATURES = {
     ),
     "jq_mx_dequantize": (_I, [_P, _P, _I, _L, _L, _P, _I, _P]),
     "jq_mx_quantized_matmul": (_I, [_P, _I, _P, _P, _I, _L, _L, _L, _P, _I, _P]),
+    "jq_moe_experts": (
+        _I,
+        [_P, _I, _L, _L, _L, _L, _P, _I, _I, _P, _P,
+         _P, _P, _P, _P, _P, _P, _I,
+         _P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _L, _P],
+    ),
     "jq_switch_glu_combine": (
         _I,
         [_P, _I, _L, _L, _L, _L, _P, _P, _I,

@@ -19,6 +19,7 @@
 // per-group affine sum s * sum q x + b * sum x (jang-tools/jang_tools/dsv41/metal_decode.py:202-233).
 #include "jq_gemv.h"
 #include "jq_qmv.h"
+#include "jq_route.h"
 
 namespace {
 
@@ -42,7 +43,16 @@ struct GatherArgs {
   const void* cshared;
   void* cout;
   int ck, ctok;
+  // Routed form (direct pairs t*rk + j of a launch that routes for itself): pair t*rk + j
+  // uses the j-th expert of top-rk(softmax(rlogits[t])); the token's ids and weights go to
+  // ridx / rw (for the launches that follow).
+  const float* rlogits;
+  uint32_t* ridx;
+  float* rw;
+  int rE, rk, rrenorm;
 };
+
+constexpr int kRouteSlots = 8;  // routed form: up to 64 * 8 = 512 experts
 
 JQ_DEV float round_out(float v, int yd) {
   if (yd == JQ_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
@@ -122,7 +132,9 @@ JQ_DEV float group_total(float v) {
 // COMB: the combined form above. Items are (token, row block); wave j of a block computes
 // expert slot j's rows of the item over the whole of K (the waves do not split K), and wave 0
 // sums the k slot outputs of each row in slot order.
-template <class D, int SB, int MT, int RBL, int NB, int RW, bool COMB = false>
+// ROUTE: the routed form above; every wave computes its token's top-k (kept in its lanes,
+// recomputed when the token changes) instead of reading expert ids.
+template <class D, int SB, int MT, int RBL, int NB, int RW, bool COMB = false, bool ROUTE = false>
 __global__ void __launch_bounds__(64 * (COMB ? kMaxCombSlots : kMaxWaves))
 gemv_gather_kernel(GatherArgs a) {
   constexpr int BITS = D::BITS;
@@ -222,7 +234,37 @@ gemv_gather_kernel(GatherArgs a) {
     tile = it / a.nrb;
     rbi = it - tile * a.nrb;
   }
-  int4 tl = get_tile(a.plan, tile);
+  // Routed form: lane j holds expert j (and its weight) of token rt_tok.
+  int rt_tok = -1;
+  uint32_t rt_id = 0;
+  float rt_w = 0.f;
+  auto tile_of = [&](int t) -> int4 {
+    if constexpr (ROUTE) {
+      const int tok = t / a.rk, j = t - tok * a.rk;
+      if (tok != rt_tok) {  // wave-uniform
+        jqr::route_wave<kRouteSlots>(a.rlogits + (int64_t)tok * a.rE, a.rE, a.rk, a.rrenorm,
+                                     lane, rt_id, rt_w);
+        rt_tok = tok;
+      }
+      const uint32_t e = (uint32_t)__builtin_amdgcn_readlane((int)rt_id, j);
+      const bool ok = e < (uint32_t)a.plan.E;
+      return make_int4(ok ? (int)e : 0, 0, ok ? 1 : 0, t);
+    } else {
+      return get_tile(a.plan, t);
+    }
+  };
+  // The token's ids and weights, once per token: by wave 0 of the item (pair t*rk, row block 0).
+  auto publish = [&](int t, int rb) {
+    if constexpr (ROUTE) {
+      const int tok = t / a.rk;
+      if (t == tok * a.rk && rb == 0 && wave == 0 && lane < a.rk) {
+        a.ridx[(int64_t)tok * a.rk + lane] = rt_id;
+        a.rw[(int64_t)tok * a.rk + lane] = rt_w;
+      }
+    }
+  };
+  int4 tl = tile_of(tile);
+  publish(tile, rbi);
   TileRows<MT> tr;
   tile_rows<MT>(a.plan, tl, tr);
   int64_t row0 = (int64_t)rbi * ROWS;
@@ -244,7 +286,8 @@ gemv_gather_kernel(GatherArgs a) {
     const int tile2 = more && wrap ? tile + (COMB ? a.ck : 1) : tile;
     const int rbi2 = more ? (wrap ? 0 : rbi + 1) : rbi;
     const int ct2 = more && wrap ? ct + 1 : ct;
-    const int4 tl2 = get_tile(a.plan, tile2);
+    const int4 tl2 = tile_of(tile2);
+    if (more) publish(tile2, rbi2);
     const int64_t row02 = (int64_t)rbi2 * ROWS;
     Rsrc rc2[NB], rs2[NB], rb2[NB];
     views(tl2, row02, more, rc2, rs2, rb2);
@@ -329,7 +372,7 @@ gemv_gather_kernel(GatherArgs a) {
   }
 }
 
-template <class D, int SB, int MT, int RBL, int NB, int RW, bool COMB = false>
+template <class D, int SB, int MT, int RBL, int NB, int RW, bool COMB = false, bool ROUTE = false>
 int launch_g(GatherArgs& a, int64_t max_tiles, hipStream_t st) {
   int kws = 0;
   int kw = RW == 1 ? gemv_waves(a.p[0].K, D::BITS, &kws) : 1;
@@ -348,7 +391,7 @@ int launch_g(GatherArgs& a, int64_t max_tiles, hipStream_t st) {
   const int64_t units = COMB ? (int64_t)a.ctok * nrb : max_items;  // block ranges
   int nb = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &nb, gemv_gather_kernel<D, SB, MT, RBL, NB, RW, COMB>, 64 * kw, 0) != hipSuccess ||
+          &nb, gemv_gather_kernel<D, SB, MT, RBL, NB, RW, COMB, ROUTE>, 64 * kw, 0) != hipSuccess ||
       nb < 1)
     nb = 1;
   int dev = 0, cus = 256;
@@ -357,7 +400,7 @@ int launch_g(GatherArgs& a, int64_t max_tiles, hipStream_t st) {
     cus = 256;
   const int64_t cap = (int64_t)nb * cus;
   const int grid = (int)(units < cap ? units : cap);
-  gemv_gather_kernel<D, SB, MT, RBL, NB, RW, COMB><<<grid, 64 * kw, 0, st>>>(a);
+  gemv_gather_kernel<D, SB, MT, RBL, NB, RW, COMB, ROUTE><<<grid, 64 * kw, 0, st>>>(a);
   return jqh::launch_status();
 }
 
@@ -366,6 +409,10 @@ int launch_g(GatherArgs& a, int64_t max_tiles, hipStream_t st) {
 template <class D, int SB, int NB, int RW>
 int launch_rw(GatherArgs& a, int mt, int64_t max_tiles, hipStream_t st) {
   constexpr int RBL = 4 * NB;
+  if (a.rlogits) {
+    if constexpr (NB == 2) return launch_g<D, SB, 1, RBL, NB, RW, false, true>(a, max_tiles, st);
+    return JQ_ERR_SHAPE;
+  }
   if (a.cout) {
     if constexpr (NB == 1) return launch_g<D, SB, 1, RBL, NB, RW, true>(a, max_tiles, st);
     return JQ_ERR_SHAPE;
@@ -445,6 +492,10 @@ int gemv_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPl
   a.cshared = nullptr;
   a.cout = nullptr;
   a.ck = a.ctok = 0;
+  a.rlogits = nullptr;
+  a.ridx = nullptr;
+  a.rw = nullptr;
+  a.rE = a.rk = a.rrenorm = 0;
   if (p2) return launch_bits<2>(a, bits, xd, sb, tile_rows, max_tiles, st);
   return launch_bits<1>(a, bits, xd, sb, tile_rows, max_tiles, st);
 }
@@ -475,7 +526,43 @@ int gemv_gather_comb_launch(const QmmProblem& p, const GatherPlan& plan, const f
   a.cout = out;
   a.ck = k;
   a.ctok = (int)T;
+  a.rlogits = nullptr;
+  a.ridx = nullptr;
+  a.rw = nullptr;
+  a.rE = a.rk = a.rrenorm = 0;
   return launch_bits<1>(a, bits, xd, sb, 1, T * k, st);
+}
+
+bool gemv_gather_route_ok(int64_t E, int k) {
+  return E >= 1 && E <= 64 * kRouteSlots && k >= 1 && k <= 64 && k <= E;
+}
+
+int gemv_gather_route_launch(const QmmProblem& g, const QmmProblem& u, const GatherPlan& plan,
+                             const float* logits, int64_t E, int k, int renorm, uint32_t* idx,
+                             float* w, int64_t T, int bits, int gs, int xd, int sb, int yd,
+                             hipStream_t st) {
+  if (T == 0 || g.N == 0) return JQ_OK;
+  if (!gemv_gather_route_ok(E, k) || !gemv_gather_ok(g.N, g.K, bits, gs, xd, sb) ||
+      plan.tiles || plan.lhs || plan.direct_rows != 1 || plan.direct_pairs != T * k ||
+      plan.pair_div != k || plan.E != E || !logits || !idx || !w)
+    return JQ_ERR_SHAPE;
+  GatherArgs a;
+  a.p[0] = g;
+  a.p[1] = u;
+  a.plan = plan;
+  a.ushift = gs == 32 ? 0 : gs == 64 ? 1 : 2;
+  a.yd = yd;
+  a.cw = nullptr;
+  a.cshared = nullptr;
+  a.cout = nullptr;
+  a.ck = a.ctok = 0;
+  a.rlogits = logits;
+  a.ridx = idx;
+  a.rw = w;
+  a.rE = (int)E;
+  a.rk = k;
+  a.rrenorm = renorm;
+  return launch_bits<2>(a, bits, xd, sb, 1, T * k, st);
 }
 
 }  // namespace jqk

@@ -13,6 +13,7 @@
 #include "jq_common.h"
 #include "jq_gemv.h"
 #include "jq_qmv.h"
+#include "jq_route.h"
 
 namespace {
 
@@ -26,59 +27,7 @@ constexpr int kGemmTileRows = 16;
 constexpr int64_t kGemvRows = 4096;
 constexpr int kMaxExperts = 4096;
 
-// Order-preserving u32 key of a float (a larger float has a larger key; -0 is taken as +0
-// by the caller); 0 lies below every float's key and marks chosen or padding slots.
-JQ_DEV uint32_t ord_key(float v) {
-  const uint32_t b = __float_as_uint(v);
-  return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
-}
-JQ_DEV float ord_val(uint32_t k) {
-  return __uint_as_float(k & 0x80000000u ? k ^ 0x80000000u : ~k);
-}
-
-// One DPP step of a wave maximum (lanes outside row_mask, and lanes whose source is out of
-// range, see the neutral value and keep theirs).
-template <int CTRL, int ROWS>
-JQ_DEV uint64_t max_step(uint64_t k) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)k, CTRL, ROWS, 0xF, false);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(k >> 32), CTRL, ROWS, 0xF, false);
-  const uint64_t o = ((uint64_t)hi << 32) | lo;
-  return o > k ? o : k;
-}
-template <int CTRL, int ROWS>
-JQ_DEV float fmax_step(float v) {
-  return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                      __builtin_bit_cast(int, -INFINITY), __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false)));
-}
-
-// Wave maxima, broadcast to every lane: DPP row operations carry the maximum into lane 63
-// (as a wave sum would), a scalar read hands it to all lanes.
-JQ_DEV uint64_t wave_max_u64(uint64_t k) {
-  k = max_step<0xB1, 0xF>(k);   // quad_perm 1,0,3,2
-  k = max_step<0x4E, 0xF>(k);   // quad_perm 2,3,0,1
-  k = max_step<0x124, 0xF>(k);  // row_ror 4
-  k = max_step<0x128, 0xF>(k);  // row_ror 8
-  k = max_step<0x142, 0xA>(k);  // row_bcast 15
-  k = max_step<0x143, 0xC>(k);  // row_bcast 31
-  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)k, 63);
-  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
-  return ((uint64_t)hi << 32) | lo;
-}
-JQ_DEV float wave_max_f32(float v) {
-  v = fmax_step<0xB1, 0xF>(v);
-  v = fmax_step<0x4E, 0xF>(v);
-  v = fmax_step<0x124, 0xF>(v);
-  v = fmax_step<0x128, 0xF>(v);
-  v = fmax_step<0x142, 0xA>(v);
-  v = fmax_step<0x143, 0xC>(v);
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
-// One wave per token. Lane l holds the order keys of logits l, l + 64, ... (SL = ceil(E/64)
-// of them); probabilities from a max-subtracted fp32 softmax. Top-k in k rounds on the
-// logits (softmax is monotone): each lane offers its largest remaining key and the wave
-// maximum of (key, ~id) picks the round's expert (ties -> lowest id), whose key is then
-// cleared. Lane j keeps round j's pick; the k probabilities are formed at the end.
+// One wave per token (jqr::route_wave).
 template <int SL>
 __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ logits, int T, int E,
                                                     int k, int renorm, uint32_t* __restrict__ idx,
@@ -86,49 +35,12 @@ __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ lo
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  const float* row = logits + (int64_t)t * E;
-  uint32_t key[SL];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < SL; ++i) {
-    const int e = lane + 64 * i;
-    const float v = e < E ? row[e] + 0.0f : -INFINITY;  // + 0: -0 becomes +0
-    key[i] = e < E ? ord_key(v) : 0u;
-    mx = fmaxf(mx, v);
-  }
-  mx = wave_max_f32(mx);
-  float sum = 0.f;
-#pragma unroll
-  for (int i = 0; i < SL; ++i) sum += key[i] ? expf(ord_val(key[i]) - mx) : 0.f;
-  sum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                      __builtin_bit_cast(int, jqg::wave_total_lane63(sum)), 63));
-  const float inv = 1.0f / sum;
-
-  uint64_t mine = 0;  // lane j: round j's (key, ~id)
-  for (int j = 0; j < k; ++j) {
-    // The lane's largest remaining key; a strict > in slot order keeps the lowest id.
-    uint32_t bk = 0;
-    int bi = 0;
-#pragma unroll
-    for (int i = 0; i < SL; ++i) {
-      const bool better = key[i] > bk;
-      bk = better ? key[i] : bk;
-      bi = better ? i : bi;
-    }
-    const uint64_t offer = bk ? ((uint64_t)bk << 32) | (uint32_t)~(uint32_t)(lane + 64 * bi) : 0ull;
-    const uint64_t best = wave_max_u64(offer);
-    const uint32_t bid = ~(uint32_t)best;
-#pragma unroll
-    for (int i = 0; i < SL; ++i) key[i] = (uint32_t)(lane + 64 * i) == bid ? 0u : key[i];
-    mine = lane == j ? best : mine;
-  }
-  const float p = expf(ord_val((uint32_t)(mine >> 32)) - mx) * inv;
-  float wsum = 0.f;  // the k probabilities in round order
-  for (int j = 0; j < k; ++j)
-    wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), j));
+  uint32_t id;
+  float w;
+  jqr::route_wave<SL>(logits + (int64_t)t * E, E, k, renorm, lane, id, w);
   if (lane < k) {
-    idx[(int64_t)t * k + lane] = ~(uint32_t)mine;
-    wout[(int64_t)t * k + lane] = renorm ? p / wsum : p;
+    idx[(int64_t)t * k + lane] = id;
+    wout[(int64_t)t * k + lane] = w;
   }
 }
 
@@ -560,7 +472,8 @@ static int switch_glu_run(const void* x, int x_dtype, int64_t T, int64_t H, int6
                           const void* down_biases, int bits_d, int sb_dtype, int group_size,
                           void* h_buf, void* out, int y_dtype, void* workspace,
                           int64_t workspace_bytes, const float* cw, const void* cshared,
-                          void* comb_out, hipStream_t st) {
+                          void* comb_out, hipStream_t st, const float* rlogits = nullptr,
+                          int renorm = 1) {
   int s = check_expert_shape(bits_gu, group_size, E, I, H);
   if (s) return s;
   s = check_expert_shape(bits_d, group_size, E, H, I);
@@ -577,6 +490,7 @@ static int switch_glu_run(const void* x, int x_dtype, int64_t T, int64_t H, int6
     return JQ_ERR_NULL;
   if (comb_out && !cw) return JQ_ERR_NULL;
   if (!workspace || workspace_bytes < ws_layout(n_pairs, E, 1).total) return JQ_ERR_WORKSPACE;
+  // With logits, idx and cw are outputs: the routing of the T tokens.
   // Pair i = t*k + j uses x row t = i / k and expert idx[i]; one plan serves both launches
   // (gate+up reads x rows i / k, down reads h rows i).
   const int bv[2] = {bits_gu, bits_d};
@@ -584,6 +498,14 @@ static int switch_glu_run(const void* x, int x_dtype, int64_t T, int64_t H, int6
   const Choice c = choose(n_pairs, E, n_pairs, group_size, x_dtype, sb_dtype, 2, bv, Nv, Kv);
   jqk::GatherPlan plan;
   const bool direct = c.k == Kern::gemv && c.tile_rows == 1;
+  // Routing inside the gate|up launch: decode sizes with the combine fused into the down
+  // launch, so that the three MoE launches after the router become two.
+  const bool self_route = rlogits && direct && comb_out && jqk::gemv_gather_route_ok(E, k) &&
+                          jqk::gemv_gather_comb_ok(T, k, H, I, bits_d, group_size, y_dtype, sb_dtype);
+  if (rlogits && !self_route) {
+    s = jq_moe_route(rlogits, T, E, k, renorm, (uint32_t*)idx, (float*)cw, (jq_stream_t)st);
+    if (s) return s;
+  }
   if (direct) {
     plan = direct_plan(idx, n_pairs, E, nullptr);
   } else {
@@ -603,7 +525,12 @@ static int switch_glu_run(const void* x, int x_dtype, int64_t T, int64_t H, int6
   u = g;
   u.codes = up_codes; u.scales = up_scales; u.biases = up_biases;
   const int64_t mt = direct ? n_pairs : max_tiles_for(n_pairs, E, 1, c.tile_rows);
-  s = grouped_launch(c, g, &u, plan_gu, mt, bits_gu, group_size, x_dtype, sb_dtype, y_dtype, st);
+  if (self_route)
+    s = jqk::gemv_gather_route_launch(g, u, plan_gu, rlogits, E, k, renorm, (uint32_t*)idx,
+                                      (float*)cw, T, bits_gu, group_size, x_dtype, sb_dtype,
+                                      y_dtype, st);
+  else
+    s = grouped_launch(c, g, &u, plan_gu, mt, bits_gu, group_size, x_dtype, sb_dtype, y_dtype, st);
   if (s) return s;
   d.x = h_buf; d.codes = down_codes; d.scales = down_scales; d.biases = down_biases; d.y = out;
   d.M = 1; d.N = H; d.K = I;
@@ -630,6 +557,23 @@ int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, i
                         down_biases, bits_d, sb_dtype, group_size, h_buf, out, y_dtype,
                         workspace, workspace_bytes, nullptr, nullptr, nullptr,
                         (hipStream_t)stream);
+}
+
+int jq_moe_experts(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E,
+                   const float* logits, int k, int renorm, uint32_t* idx, float* weights,
+                   const uint32_t* gate_codes, const void* gate_scales, const void* gate_biases,
+                   const uint32_t* up_codes, const void* up_scales, const void* up_biases,
+                   int bits_gu, const uint32_t* down_codes, const void* down_scales,
+                   const void* down_biases, int bits_d, int sb_dtype, int group_size,
+                   void* h_buf, void* y_buf, const void* shared, void* out, int y_dtype,
+                   void* workspace, int64_t workspace_bytes, jq_stream_t stream) {
+  if (T > 0 && (!logits || !idx || !weights || !out)) return JQ_ERR_NULL;
+  if (E <= 0 || E > kMaxExperts || k <= 0 || k > E || k > 64) return JQ_ERR_SHAPE;
+  return switch_glu_run(x, x_dtype, T, H, I, E, idx, k, gate_codes, gate_scales, gate_biases,
+                        up_codes, up_scales, up_biases, bits_gu, down_codes, down_scales,
+                        down_biases, bits_d, sb_dtype, group_size, h_buf, y_buf, y_dtype,
+                        workspace, workspace_bytes, weights, shared, out, (hipStream_t)stream,
+                        logits, renorm);
 }
 
 int jq_switch_glu_combine(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,

@@ -138,5 +138,13 @@ bool gemv_gather_comb_ok(int64_t T, int k, int64_t N, int64_t K, int bits, int g
 int gemv_gather_comb_launch(const QmmProblem& p, const GatherPlan& plan, const float* w,
                             const void* shared, void* out, int64_t T, int k, int bits, int gs,
                             int xd, int sb, int yd, hipStream_t st);
+// The gate|up launch over a direct plan of T * k pairs (x row = pair / k) that routes for
+// itself: pair t*k + j takes the j-th expert of top-k(softmax(logits[t])) (E <= 512), and the
+// token's ids and weights are written to idx / w [T, k] as jq_moe_route writes them.
+bool gemv_gather_route_ok(int64_t E, int k);
+int gemv_gather_route_launch(const QmmProblem& g, const QmmProblem& u, const GatherPlan& plan,
+                             const float* logits, int64_t E, int k, int renorm, uint32_t* idx,
+                             float* w, int64_t T, int bits, int gs, int xd, int sb, int yd,
+                             hipStream_t st);
 
 }  // namespace jqk

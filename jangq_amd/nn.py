@@ -157,10 +157,11 @@ class SparseMoeBlock(torch.nn.Module):
         shared = self.shared_expert(x) if self.shared_expert is not None else None
         if logits is None:
             logits = self.gate(x).float()
-        inds, scores = ops.moe_route(logits, self.top_k, self.norm_topk_prob)
-        # switch_mlp, then (y * scores[..., None]).sum(-2) (+ shared), qwen4_exp/modeling.py:594-597;
-        # one call, so that at decode sizes the combine runs inside the down-projection launch.
+        # top-k routing, switch_mlp, then (y * scores[..., None]).sum(-2) (+ shared),
+        # qwen4_exp/modeling.py:587-597, as one call: at decode sizes the gate|up launch routes
+        # for itself and the combine runs inside the down-projection launch.
         m = self.switch_mlp
-        return ops.switch_glu_combine(x, inds, scores, m.gate_proj.as_tuple(),
-                                      m.up_proj.as_tuple(), m.down_proj.as_tuple(),
-                                      m.group_size(), shared)
+        out, _, _ = ops.moe_experts(x, logits, self.top_k, m.gate_proj.as_tuple(),
+                                    m.up_proj.as_tuple(), m.down_proj.as_tuple(),
+                                    m.group_size(), shared, self.norm_topk_prob)
+        return out

@@ -426,6 +426,51 @@ def switch_glu_combine(x: torch.Tensor, indices: torch.Tensor, weights: torch.Te
     return out
 
 
+def moe_experts(x: torch.Tensor, logits: torch.Tensor, k: int, gate, up, down,
+                group_size: int = 64, shared: torch.Tensor | None = None,
+                renorm: bool = True):
+    """moe_route(logits, k, renorm) then switch_glu_combine(x, ...) with its ids and scores:
+    the MoE block after the router GEMV (qwen4_exp/modeling.py:587-597). Returns
+    (out, ids, scores). At decode sizes the gate|up launch routes for itself."""
+    x = _dev(x, "x")
+    logits = _dev(logits, "logits")
+    if logits.dtype != torch.float32:
+        logits = logits.float().contiguous()
+    gw, gsc, gb, bits_gu = gate
+    uw, usc, ub, bits_u = up
+    dw, dsc, db, bits_d = down
+    if bits_u != bits_gu:
+        raise ValueError("gate and up projections must share a bit width")
+    _check_bits_gs(bits_gu, group_size)
+    _check_bits_gs(bits_d, group_size)
+    gw, uw, dw = _codes(gw), _codes(uw), _codes(dw)
+    E, I = gw.shape[0], gw.shape[1]
+    H = x.shape[-1]
+    if packed_in_features(gw, bits_gu) != H or dw.shape[1] != H or packed_in_features(dw, bits_d) != I:
+        raise ValueError("expert weight shapes do not match x / each other")
+    T = math.prod(x.shape[:-1])
+    if tuple(logits.shape) != (*x.shape[:-1], E):
+        raise ValueError(f"logits must be {(*x.shape[:-1], E)}, got {tuple(logits.shape)}")
+    if shared is not None:
+        shared = _dev(shared, "shared")
+        if tuple(shared.shape) != tuple(x.shape) or shared.dtype != x.dtype:
+            raise ValueError("shared must match x's shape and dtype")
+    idx = torch.empty((*x.shape[:-1], k), dtype=torch.int32, device=x.device)
+    w = torch.empty((*x.shape[:-1], k), dtype=torch.float32, device=x.device)
+    h = torch.empty((T * k, I), dtype=x.dtype, device=x.device)
+    ybuf = torch.empty((T * k, H), dtype=x.dtype, device=x.device)
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    ws = _gather_workspace(T * k, E, 1, x.device)
+    _lib.check(_lib.lib().jq_moe_experts(
+        _ptr(x), _dtype_code(x, "x"), T, H, I, E, _ptr(logits), k, int(renorm), _ptr(idx),
+        _ptr(w), _ptr(gw), _ptr(_dev(gsc, "scales")), _ptr(_dev(gb, "biases")),
+        _ptr(uw), _ptr(_dev(usc, "scales")), _ptr(_dev(ub, "biases")), bits_gu,
+        _ptr(dw), _ptr(_dev(dsc, "scales")), _ptr(_dev(db, "biases")), bits_d,
+        _dtype_code(gsc, "scales"), group_size, _ptr(h), _ptr(ybuf), _ptr(shared), _ptr(out),
+        _dtype_code(out, "output"), _ptr(ws), ws.numel(), _stream()), "moe_experts")
+    return out, idx, w
+
+
 def moe_combine(y: torch.Tensor, weights: torch.Tensor,
                 shared: torch.Tensor | None = None) -> torch.Tensor:
     """sum_j weights[..., j] * y[..., j, :] in fp32 (slot order), in y.dtype, plus ``shared``

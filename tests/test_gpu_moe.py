@@ -286,3 +286,32 @@ def test_switch_glu_combine(T, k, E, H, I, bits_d, gs, with_shared, xdt):
         pre = O.round_to(pre, xdt).astype(np.float64) + sh
     assert_close(values_of(got), ref, f"switch_glu_combine T{T} k{k} E{E} {xdt}", exact=pre,
                  out_dtype=xdt)
+
+
+@pytest.mark.parametrize("T,k,E,H,I,with_shared,renorm", [
+    (1, 4, 128, 512, 256, False, True),   # config-3 class: the gate|up launch routes for itself
+    (1, 10, 512, 512, 256, True, True),   # config-5 class (top-10 of 512)
+    (3, 2, 64, 384, 128, True, False),    # several tokens, no renormalisation
+    (64, 4, 128, 256, 128, True, True),   # above decode sizes: routing launch, plan, tiles
+    (1, 4, 640, 256, 128, False, True),   # more experts than the in-launch routing holds
+])
+def test_moe_experts(T, k, E, H, I, with_shared, renorm):
+    """Routing + experts + combine in one call: ids, weights and output bit-identical to
+    moe_route followed by switch_glu_combine; ids equal to the oracle's top-k."""
+    gs = 64
+    g = _stack(E, I, H, 2, gs, seed=51)
+    u = _stack(E, I, H, 2, gs, seed=52)
+    d = _stack(E, H, I, 2, gs, seed=53)
+    rng = np.random.default_rng(T + E + k)
+    x = to_tensor(O.round_bf16(rng.standard_normal((T, H), dtype=np.float32)), "bf16")
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    tl = torch.from_numpy(logits).cuda()
+    sh = to_tensor(O.round_bf16(rng.standard_normal((T, H), dtype=np.float32)), "bf16") \
+        if with_shared else None
+    gt, ut, dt_ = (g.dw, g.ds, g.db, 2), (u.dw, u.ds, u.db, 2), (d.dw, d.ds, d.db, 2)
+    out, ids, w = jq.moe_experts(x, tl, k, gt, ut, dt_, gs, sh, renorm)
+    ids2, w2 = jq.moe_route(tl, k, renorm)
+    out2 = jq.switch_glu_combine(x, ids2, w2, gt, ut, dt_, gs, sh)
+    assert torch.equal(ids, ids2) and torch.equal(w, w2)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+    np.testing.assert_array_equal(ids.cpu().numpy(), O.route_topk(logits, k, renorm)[0])
