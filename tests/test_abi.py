@@ -64,3 +64,35 @@ def test_entry_points_validate_before_launch(native_lib):
     one = ctypes.c_void_p(1)
     assert L.jq_gather_qmm(one, 1, 4, 1, one, one, one, 1, 4, 64, 8, 128, 128, None, one, 4, 0,
                            one, 1, None, 0, None) == -7
+
+
+def test_newer_entry_points_validate_before_launch(native_lib):
+    """MX modes, the fused MoE calls and the K-split workspace query reject bad arguments on
+    the host (no launch)."""
+    L = native_lib
+    assert L.jq_mx_dequantize(None, None, 5, 1, 32, None, 0, None) == -1     # mode
+    assert L.jq_mx_dequantize(None, None, 4, 1, 48, None, 0, None) == -2     # K % 32
+    assert L.jq_mx_dequantize(None, None, 4, 1, 32, None, 0, None) == -5     # null
+    assert L.jq_mx_dequantize(None, None, 8, 0, 32, None, 0, None) == 0      # empty
+    assert L.jq_mx_quantized_matmul(None, 1, None, None, 4, 1, 8, 32 * 64 * 8 + 32, None, 1,
+                                    None) == -3                               # K too long
+    assert L.jq_mx_quantized_matmul(None, 0, None, None, 8, 1, 8, 64, None, 1, None) == -4
+    # routed experts: k > E, and missing logits with tokens to route
+    args = [None, 1, 1, 256, 128, 4, None, 5, 1, None, None,
+            None, None, None, None, None, None, 2, None, None, None, 2, 1, 64,
+            None, None, None, None, 1, None, 0, None]
+    one = ctypes.c_void_p(1)
+    a = list(args)
+    a[6], a[9], a[10], a[27] = one, one, one, one
+    assert L.jq_moe_experts(*a) == -3
+    a = list(args)
+    a[7] = 2
+    assert L.jq_moe_experts(*a) == -5
+    # fused combine: weights missing
+    assert L.jq_switch_glu_combine(None, 1, 1, 256, 128, 4, None, None, 2, None, None, None,
+                                   None, None, None, 2, None, None, None, 2, 1, 64, None, None,
+                                   None, None, 1, None, 0, None) == -5
+    # K-split workspace: 0 where the split does not apply, -1 for negative sizes
+    assert L.jq_quantized_matmul_workspace_size(1, 4096, 4096, 4, 64, 1, 1) == 0
+    assert L.jq_quantized_matmul_workspace_size(8, 4096, 14336, 2, 64, 1, 1) > 0
+    assert L.jq_quantized_matmul_workspace_size(-1, 4096, 14336, 2, 64, 1, 1) == -1
