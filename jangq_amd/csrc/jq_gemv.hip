@@ -208,8 +208,12 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_kernel(GemvArgs a) {
 // every row, so a row's sum is one DPP wave reduction and no LDS or barrier is involved. The
 // waves (4 per block) are independent and persistent over row blocks of RB rows, with the
 // same rolling register ring as gemv_kernel.
-template <class D, int SB, int CPL, int RB>
+// GLU: problems 0 and 1 are the gate and up projections of a SwiGLU pair (same N); an item
+// is row n of each (RB = 2), and the wave stores h[n] = silu(round(g)) * round(u) to
+// problem 0's output.
+template <class D, int SB, int CPL, int RB, bool GLU = false>
 __global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a) {
+  static_assert(!GLU || RB == 2, "a SwiGLU item is one row of gate and one of up");
   constexpr int BITS = D::BITS;
   constexpr int UPL = units_per_chunk<BITS>();
   constexpr int NW = BITS * UPL;
@@ -242,6 +246,10 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a) {
                      xr[j][t]);
   auto locate = [&](int i, int& p, int64_t& row0) {
     p = 0;
+    if constexpr (GLU) {
+      row0 = i;
+      return;
+    }
 #pragma unroll
     for (int q = 1; q < jqk::kMaxProblems; ++q)
       if (q < a.nprob && i >= a.rb_begin[q]) p = q;
@@ -250,7 +258,8 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a) {
   auto views = [&](int p, int64_t row0, bool live, Rsrc& rc, Rsrc& rs, Rsrc& rb) {
     const QmvProblem& pb = a.b.p[p];
     const int64_t left = pb.N - row0;
-    const uint32_t rows = live ? (uint32_t)(left < RB ? left : RB) : 0u;
+    constexpr int VR = GLU ? 1 : RB;  // rows of one view
+    const uint32_t rows = live ? (uint32_t)(left < VR ? left : VR) : 0u;
     rc = make_rsrc((const char*)pb.codes + row0 * rowbytes, rows * rowbytes);
     rs = make_rsrc((const char*)pb.scales + row0 * sbrow, rows * sbrow);
     rb = make_rsrc((const char*)pb.biases + row0 * sbrow, rows * sbrow);
@@ -269,12 +278,14 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a) {
   int p;
   int64_t row0;
   locate(it, p, row0);
-  Rsrc rc, rs, rbv;
+  Rsrc rc, rs, rbv, rcu, rsu, rbu;  // (up views: GLU only)
   views(p, row0, true, rc, rs, rbv);
+  if constexpr (GLU) views(1, row0, true, rcu, rsu, rbu);
   RowSlot<NW, UPL> ring[RB][CPL];
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
-    load_row(rc, rs, rbv, r, ring[r]);
+    if (GLU && r == 1) load_row(rcu, rsu, rbu, 0, ring[r]);
+    else load_row(rc, rs, rbv, GLU ? 0 : r, ring[r]);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -295,8 +306,9 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a) {
     int p2;
     int64_t row02;
     locate(more ? nx : it, p2, row02);
-    Rsrc rc2, rs2, rb2;
+    Rsrc rc2, rs2, rb2, rcu2, rsu2, rbu2;
     views(p2, row02, more, rc2, rs2, rb2);
+    if constexpr (GLU) views(1, row02, more, rcu2, rsu2, rbu2);
     float acc[RB];
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
@@ -311,18 +323,32 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a) {
           acc[r] = fmaf(sv, d + xs[j][t].O, fmaf(bv, xs[j][t].X, acc[r]));
         }
       asm volatile("" : "+v"(acc[r])::"memory");
-      load_row(rc2, rs2, rb2, r, ring[r]);
+      if (GLU && r == 1) load_row(rcu2, rsu2, rbu2, 0, ring[r]);
+      else load_row(rc2, rs2, rb2, GLU ? 0 : r, ring[r]);
       __builtin_amdgcn_sched_barrier(0);
     }
     const QmvProblem& pb = a.b.p[p];
+    if constexpr (GLU) {
+      const float gt = wave_total_lane63(acc[0]), ut = wave_total_lane63(acc[1]);
+      if (lane == 63 && row0 < pb.N) {
+        // g and u rounded to the output type first, as two matmuls returning it would be
+        const bool bf = a.yd == JQ_BF16;
+        const float g = bf ? bf16_bits_to_f32(f32_to_bf16_bits(gt)) : f16_bits_to_f32(f32_to_f16_bits(gt));
+        const float u = bf ? bf16_bits_to_f32(f32_to_bf16_bits(ut)) : f16_bits_to_f32(f32_to_f16_bits(ut));
+        const float hv = g / (1.0f + expf(-g)) * u;
+        if (bf) store_t<JQ_BF16>(pb.y, row0, hv);
+        else store_t<JQ_F16>(pb.y, row0, hv);
+      }
+    } else {
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const float v = wave_total_lane63(acc[r]);
-      const int64_t row = row0 + r;
-      if (lane == 63 && row < pb.N) {
-        if (a.yd == JQ_BF16) store_t<JQ_BF16>(pb.y, row, v);
-        else if (a.yd == JQ_F16) store_t<JQ_F16>(pb.y, row, v);
-        else store_t<JQ_F32>(pb.y, row, v);
+      for (int r = 0; r < RB; ++r) {
+        const float v = wave_total_lane63(acc[r]);
+        const int64_t row = row0 + r;
+        if (lane == 63 && row < pb.N) {
+          if (a.yd == JQ_BF16) store_t<JQ_BF16>(pb.y, row, v);
+          else if (a.yd == JQ_F16) store_t<JQ_F16>(pb.y, row, v);
+          else store_t<JQ_F32>(pb.y, row, v);
+        }
       }
     }
     if (!more) break;
@@ -332,18 +358,24 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a) {
   }
 }
 
-template <class D, int SB, int CPL, int RB>
+template <class D, int SB, int CPL, int RB, bool GLU = false>
 int launch_row(GemvArgs& a, hipStream_t st) {
   a.kwshift = 0;
   int total = 0;
-  for (int i = 0; i < a.nprob; ++i) {
-    a.rb_begin[i] = total;
-    total += (int)((a.b.p[i].N + RB - 1) / RB);
+  if constexpr (GLU) {  // items are rows of the pair
+    total = (int)a.b.p[0].N;
+    a.rb_begin[0] = 0;
+    for (int i = 1; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
+  } else {
+    for (int i = 0; i < a.nprob; ++i) {
+      a.rb_begin[i] = total;
+      total += (int)((a.b.p[i].N + RB - 1) / RB);
+    }
+    for (int i = a.nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
   }
-  for (int i = a.nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
   if (total == 0) return JQ_OK;
   int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_row_kernel<D, SB, CPL, RB>, 256, 0) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_row_kernel<D, SB, CPL, RB, GLU>, 256, 0) !=
           hipSuccess || nb < 1)
     nb = 1;
   int dev = 0, cus = 256;
@@ -353,7 +385,7 @@ int launch_row(GemvArgs& a, hipStream_t st) {
   const int64_t cap = (int64_t)nb * cus * 4;  // waves
   const int64_t iters = (total + cap - 1) / cap;
   const int64_t waves = (total + iters - 1) / iters;
-  gemv_row_kernel<D, SB, CPL, RB><<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(a);
+  gemv_row_kernel<D, SB, CPL, RB, GLU><<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(a);
   return jqh::launch_status();
 }
 
@@ -406,6 +438,21 @@ int launch_m(GemvArgs& a, hipStream_t st) {
   if (a.b.M == 2) return launch_rb<D, SB, 2, 4>(a, st);
   if constexpr (!two) return launch_rb<D, SB, 4, 4>(a, st);
   return JQ_ERR_SHAPE;
+}
+
+template <class D, int SB>
+int launch_glu(GemvArgs& a, hipStream_t st) {
+  const int kw = gemv_waves(a.b.K, D::BITS, nullptr);
+  if (a.b.M != 1 || kw > 2) return JQ_ERR_SHAPE;
+  if (kw == 1) return launch_row<D, SB, 1, 2, true>(a, st);
+  return launch_row<D, SB, 2, 2, true>(a, st);
+}
+
+template <int BITS, int XDT>
+int launch_glu_sb(GemvArgs& a, int sb, hipStream_t st) {
+  using D = Dc<BITS, 64, XDT>;
+  if (sb == JQ_BF16) return launch_glu<D, JQ_BF16>(a, st);
+  return launch_glu<D, JQ_F16>(a, st);
 }
 
 template <int BITS, int XDT>
@@ -466,6 +513,36 @@ int gemv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, 
     case 6: return launch_x<6>(a, xd, sb, st);
     default: return launch_x<8>(a, xd, sb, st);
   }
+}
+
+bool gemv_swiglu_ok(int M, int64_t K, int64_t N, int bits, int gs, int xd, int sb, int yd) {
+  return M == 1 && (yd == JQ_BF16 || yd == JQ_F16) && gemv_ok(1, K, N, bits, gs, xd, sb) &&
+         gemv_waves(K, bits, nullptr) <= 2;
+}
+
+int gemv_swiglu_launch(const QmvBatch& b, int bits, int gs, int xd, int sb, int yd,
+                       hipStream_t st) {
+  if (b.p[0].N == 0) return JQ_OK;
+  if (!gemv_swiglu_ok(b.M, b.K, b.p[0].N, bits, gs, xd, sb, yd) || b.p[1].N != b.p[0].N ||
+      b.p[1].x != b.p[0].x)
+    return JQ_ERR_SHAPE;
+  GemvArgs a;
+  a.b = b;
+  a.nprob = 2;
+  a.ushift = gs == 32 ? 0 : gs == 64 ? 1 : 2;
+  a.yd = yd;
+#define JQ_GLU(B)                                                     \
+  if (xd == JQ_BF16) return launch_glu_sb<B, JQ_BF16>(a, sb, st);     \
+  return launch_glu_sb<B, JQ_F16>(a, sb, st);
+  switch (bits) {
+    case 2: { JQ_GLU(2) }
+    case 3: { JQ_GLU(3) }
+    case 4: { JQ_GLU(4) }
+    case 5: { JQ_GLU(5) }
+    case 6: { JQ_GLU(6) }
+    default: { JQ_GLU(8) }
+  }
+#undef JQ_GLU
 }
 
 }  // namespace jqk

@@ -353,6 +353,17 @@ int jq_quantized_swiglu(const void* x, int x_dtype, int64_t M, int64_t N, int64_
       !up_biases || !h)
     return JQ_ERR_NULL;
   hipStream_t st = (hipStream_t)stream;
+  // One activation row: the whole-rows-per-wave GEMV with the SiLU * up epilogue.
+  if (jqk::gemv_swiglu_ok((int)M, K, N, bits, group_size, x_dtype, sb_dtype, y_dtype)) {
+    jqk::QmvBatch b;
+    b.M = 1;
+    b.K = (int)K;
+    b.p[0].x = x; b.p[0].codes = gate_codes; b.p[0].scales = gate_scales;
+    b.p[0].biases = gate_biases; b.p[0].y = h; b.p[0].N = N;
+    b.p[1] = b.p[0];
+    b.p[1].codes = up_codes; b.p[1].scales = up_scales; b.p[1].biases = up_biases;
+    return jqk::gemv_swiglu_launch(b, bits, group_size, x_dtype, sb_dtype, y_dtype, st);
+  }
   // Decode sizes: one grouped launch of the expert-gathered GEMV over a single "expert" whose
   // tile holds all M rows, with the SiLU * up epilogue.
   const int maxr = jqk::gemv_gather_max_rows(bits);

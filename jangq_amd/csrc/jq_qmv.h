@@ -28,6 +28,11 @@ int qmv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, i
                hipStream_t st);
 
 // Decode GEMV on the vector ALUs (jq_gemv.hip): M <= 4, bf16/f16 activations and scales.
+// SwiGLU pair at one activation row (b.p[0] gate, b.p[1] up, same x and N): whole rows per
+// wave, h = silu(round(g)) * round(u) written to b.p[0].y (bf16/f16).
+bool gemv_swiglu_ok(int M, int64_t K, int64_t N, int bits, int gs, int xd, int sb, int yd);
+int gemv_swiglu_launch(const QmvBatch& b, int bits, int gs, int xd, int sb, int yd,
+                       hipStream_t st);
 bool gemv_ok(int M, int64_t K, int64_t maxN, int bits, int gs, int xd, int sb);
 int gemv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
                 hipStream_t st);
