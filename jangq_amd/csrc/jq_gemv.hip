@@ -425,13 +425,22 @@ int launch_rb(GemvArgs& a, hipStream_t st) {
 // waves of chunks runs gemv_row_kernel (whole rows per wave, 2 rows in flight), measured
 // against gemv_kernel: 4096 x 4096 4-bit 5.48 -> 5.03 us, config-2 q|k|v (6-bit) 7.40 ->
 // 7.02 us, o 5.96 -> 5.83 us, gate|up (3-bit) 13.98 -> 13.69 us; with 4 or 8 rows in flight
-// it was slower, and so were long rows (the down projection 9.12 -> 10.54 us).
+// it was slower, and so were long rows (the down projection 9.12 -> 10.54 us). Outputs of at
+// most kFewRows rows take one row per item: an 8-bit 128- or 512-expert router at K = 4096
+// 4.3 -> 3.6 us (at 4096 rows one row per item was slower, 5.2 -> 5.7 us).
+constexpr int64_t kFewRows = 1024;
 template <class D, int SB>
 int launch_m(GemvArgs& a, hipStream_t st) {
   constexpr bool two = D::BITS == 2;  // two units per lane chunk
   const int kw = gemv_waves(a.b.K, D::BITS, nullptr);
   if (a.b.M == 1) {
     if (kw >= 4) return launch_rb<D, SB, 1, 16>(a, st);
+    int64_t rows = 0;
+    for (int i = 0; i < a.nprob; ++i) rows += a.b.p[i].N;
+    if (rows <= kFewRows) {  // short outputs (routers): one row per item, twice the waves
+      if (kw == 1) return launch_row<D, SB, 1, 1>(a, st);
+      return launch_row<D, SB, 2, 1>(a, st);
+    }
     if (kw == 1) return launch_row<D, SB, 1, 2>(a, st);
     return launch_row<D, SB, 2, 2>(a, st);
   }
