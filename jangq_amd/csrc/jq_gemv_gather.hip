@@ -14,6 +14,11 @@
 // activation rows, the ring holds the next item's rows in flight while the block computes,
 // reduces and stores the current one. At a tile change the block reloads the activations.
 //
+// Two decode-size forms over direct plans (one row per pair): the combined form runs the
+// down projection with the MoE weighted combine inside (one wave per expert slot), and the
+// routed form runs gate|up with each wave computing its token's top-k from the router logits
+// instead of reading expert ids.
+//
 // Reference: gather_qmm over affine codes (mlx.core.gather_qmm as called from
 // jang-tools/jang_tools/dots3/ops.py:202-214 and jangrt/switchglu_decode.py:161-183), the
 // per-group affine sum s * sum q x + b * sum x (jang-tools/jang_tools/dsv41/metal_decode.py:202-233).
