@@ -31,7 +31,7 @@ extern "C" {
 
 typedef struct ihipStream_t* jq_stream_t; /* == hipStream_t */
 
-#define JQ_ABI_VERSION 1
+#define JQ_ABI_VERSION 2
 
 enum jq_status {
   JQ_OK = 0,
@@ -172,6 +172,51 @@ int jq_moe_route(const float* logits, int64_t T, int64_t E, int k, int renorm,
                  uint32_t* idx, float* weights, jq_stream_t stream);
 
 /*
+ * Router options (jq_moe_route_ex, jq_moe_block). A NULL options pointer means softmax scores
+ * with renormalisation (norm_topk_prob), no bias, no groups, scaling 1.
+ *   score       JQ_SCORE_SOFTMAX      softmax(logits) in fp32, max-subtracted
+ *                                     (jang-tools/jang_tools/qwen4_exp/modeling.py:587-593,
+ *                                     jang-tools/jang_tools/mistral4_mlx.py:359-387)
+ *               JQ_SCORE_SIGMOID      sigmoid(logits) (jang-tools/jang_tools/dots3/ops.py:149-162,
+ *                                     jang-tools/jang_tools/laguna/model.py:50-62)
+ *               JQ_SCORE_SQRTSOFTPLUS sqrt(softplus(logits)) (jang-tools/jang_tools/dsv41/model.py:1184-1190)
+ *   score_bias  f32 [E] device array added to the scores for the selection only
+ *               (e_score_correction_bias); the weights are the unbiased scores
+ *   n_group, topk_group  group-limited selection (n_group > 1, E % n_group == 0, n_group <= 64):
+ *               the topk_group groups of E/n_group consecutive experts with the largest
+ *               maximum selection value are kept; every other expert gets selection value 0
+ *               and score 0 (mistral4_mlx.py:363-375)
+ *   renorm      weights /= (sum of the k weights + renorm_eps): 0 for the softmax routers,
+ *               1e-20 for the sigmoid-type ones (dots3/ops.py:160, laguna/model.py:59)
+ *   scaling     routed_scaling_factor, multiplies the weights last (mistral4_mlx.py:383-385)
+ * The k experts come in descending selection order, ties to the lower expert id.
+ */
+enum jq_score_func {
+  JQ_SCORE_SOFTMAX = 0,
+  JQ_SCORE_SIGMOID = 1,
+  JQ_SCORE_SQRTSOFTPLUS = 2,
+};
+
+typedef struct jq_route_opts {
+  int score;
+  int renorm;
+  float renorm_eps;
+  float scaling;
+  const float* score_bias;
+  int n_group;
+  int topk_group;
+} jq_route_opts;
+
+/*
+ * jq_moe_route with the router options above: logits [T, E] of logits_dtype (JQ_F32, or the
+ * bf16 / f16 output of the router linear, read exactly) -> idx uint32 [T, k] and weights f32
+ * [T, k]; scores and weights are computed in fp32. E <= 4096, k <= 64.
+ * Replaces the router functions cited at jq_route_opts.
+ */
+int jq_moe_route_ex(const void* logits, int logits_dtype, int64_t T, int64_t E, int k,
+                    const jq_route_opts* opts, uint32_t* idx, float* weights, jq_stream_t stream);
+
+/*
  * Workspace bytes needed by jq_gather_qmm for n_pairs (token, expert) pairs over E experts
  * with M activation rows per pair (jq_switch_glu: M = 1, n_pairs = T*k). Host-only.
  * Returns -1 for invalid arguments.
@@ -292,6 +337,81 @@ int jq_quantized_swiglu(const void* x, int x_dtype, int64_t M, int64_t N, int64_
                         const void* up_scales, const void* up_biases, int sb_dtype, int bits,
                         int group_size, void* h, void* up_buf, int y_dtype,
                         jq_stream_t stream);
+
+/*
+ * jq_quantized_swiglu with the SwiGLU clamp of the fused MoE decode: with swiglu_limit > 0,
+ * gate = min(round(g), L) and up = clip(round(u), -L, L) before silu(gate) * up
+ * (jang-tools/jang_tools/dsv41/model.py:1239-1244 for the shared expert,
+ * jang-tools/jang_tools/dsv41/metal_decode.py:362-366).
+ */
+int jq_quantized_swiglu_ex(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
+                           const uint32_t* gate_codes, const void* gate_scales,
+                           const void* gate_biases, const uint32_t* up_codes,
+                           const void* up_scales, const void* up_biases, int sb_dtype, int bits,
+                           int group_size, float swiglu_limit, void* h, void* up_buf,
+                           int y_dtype, jq_stream_t stream);
+
+/* A quantized weight: 2-D [rows, K*bits/32], or an expert stack [E, rows, K*bits/32]. */
+typedef struct jq_qweight {
+  const uint32_t* codes;
+  const void* scales;  /* [.., rows, K/group_size] of sb_dtype */
+  const void* biases;  /* same shape and dtype */
+  int sb_dtype;
+  int bits;
+  int group_size;
+} jq_qweight;
+
+/*
+ * Where the routing weights enter a MoE block:
+ *   JQ_COMBINE_AFTER_DOWN   out = round(round(sum_j w_j * y_j) + s')   (mlx_lm / qwen-style:
+ *       jang-tools/jang_tools/qwen4_exp/modeling.py:594-599), y_j = round(down_j(h_j)),
+ *       h_j = round(silu(g_j) * u_j); s' = round(round(sigmoid(gate_logit)) * s) with a shared
+ *       gate, else s; the weighted sum is fp32 in slot order
+ *   JQ_COMBINE_BEFORE_DOWN  h_j = round(silu(g_j) * u_j * w_j), out = round(sum_j y_j + s)
+ *       (fp32, slot order; jang-tools/jang_tools/dsv41/model.py:1214-1245 and its two-dispatch
+ *       fusion, dsv41/metal_decode.py:334-503)
+ * where g_j, u_j are rounded to the activation dtype (and clamped with swiglu_limit > 0), and
+ * s = round(down_s(round(silu(g_s) * u_s))) is the shared expert's output (same clamp).
+ */
+enum jq_moe_combine_mode {
+  JQ_COMBINE_AFTER_DOWN = 0,
+  JQ_COMBINE_BEFORE_DOWN = 1,
+};
+
+typedef struct jq_moe_opts {
+  int combine;         /* jq_moe_combine_mode */
+  float swiglu_limit;  /* > 0: the SwiGLU clamp, routed and shared experts */
+} jq_moe_opts;
+
+/*
+ * Bytes of the caller workspace of jq_moe_block (-1: invalid sizes). Host-only.
+ */
+int64_t jq_moe_block_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int k,
+                                    int64_t shared_I, int x_dtype);
+
+/*
+ * A whole MoE block after the router GEMV: routing (jq_route_opts), the routed experts
+ * (SwitchGLU over gate/up/down stacks [E, I, H*b/32], [E, I, H*b/32], [E, H, I*b/32], one group
+ * size), an optional shared expert (dense SwiGLU MLP of intermediate size shared_I; NULL
+ * weights when shared_I == 0) with an optional sigmoid gate (shared_gate_logits [T] of x_dtype:
+ * the output of the 1-row shared_expert_gate linear), and the combine of jq_moe_combine_mode.
+ * x [T, H] bf16/f16; logits [T, E] of logits_dtype; outputs idx uint32 [T, k], weights f32 [T, k] (as
+ * jq_moe_route_ex writes them) and out [T, H] of x_dtype. E <= 4096, k <= 64.
+ * At decode sizes the routed experts take two launches (gate|up routing for itself, then down
+ * with the combine inside).
+ * Replaces the MoE block bodies of jang-tools/jang_tools/qwen4_exp/modeling.py:586-599,
+ * jang-tools/jang_tools/dsv41/model.py:1166-1245 (with dsv41/metal_decode.py:334-503),
+ * jang-tools/jang_tools/mistral4_mlx.py:355-387 and jang-tools/jang_tools/dots3/ops.py:149-223
+ * after their router GEMV.
+ */
+int jq_moe_block(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E, int k,
+                 const void* logits, int logits_dtype, const jq_route_opts* route,
+                 const jq_qweight* gate,
+                 const jq_qweight* up, const jq_qweight* down, int64_t shared_I,
+                 const jq_qweight* shared_gate_proj, const jq_qweight* shared_up_proj,
+                 const jq_qweight* shared_down_proj, const void* shared_gate_logits,
+                 const jq_moe_opts* opts, uint32_t* idx, float* weights, void* out,
+                 void* workspace, int64_t workspace_bytes, jq_stream_t stream);
 
 #ifdef __cplusplus
 }

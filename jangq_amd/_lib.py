@@ -61,7 +61,40 @@ SIGNATURES = {
          _P, _P, _P, _P, _P, _P, _I,
          _P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _L, _P],
     ),
+    "jq_moe_route_ex": (_I, [_P, _I, _L, _L, _I, _P, _P, _P, _P]),
+    "jq_quantized_swiglu_ex": (
+        _I,
+        [_P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _P, _I, _I, _I, C.c_float, _P, _P, _I, _P],
+    ),
+    "jq_moe_block_workspace_size": (_L, [_L, _L, _L, _L, _I, _L, _I]),
+    "jq_moe_block": (
+        _I,
+        [_P, _I, _L, _L, _L, _L, _I, _P, _I, _P, _P, _P, _P, _L, _P, _P, _P, _P, _P,
+         _P, _P, _P, _P, _L, _P],
+    ),
 }
+
+JQ_SCORE = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
+JQ_COMBINE = {"after": 0, "before": 1}
+
+
+class RouteOpts(C.Structure):
+    """jq_route_opts (include/jangq_amd.h)."""
+    _fields_ = [("score", C.c_int), ("renorm", C.c_int), ("renorm_eps", C.c_float),
+                ("scaling", C.c_float), ("score_bias", C.c_void_p), ("n_group", C.c_int),
+                ("topk_group", C.c_int)]
+
+
+class QWeight(C.Structure):
+    """jq_qweight (include/jangq_amd.h)."""
+    _fields_ = [("codes", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
+                ("sb_dtype", C.c_int), ("bits", C.c_int), ("group_size", C.c_int)]
+
+
+class MoeOpts(C.Structure):
+    """jq_moe_opts (include/jangq_amd.h)."""
+    _fields_ = [("combine", C.c_int), ("swiglu_limit", C.c_float)]
+
 
 _lib: C.CDLL | None = None
 

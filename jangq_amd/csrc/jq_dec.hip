@@ -149,7 +149,7 @@ __global__ void __launch_bounds__(64 * KW) dec_gather_kernel(QmmProblem p, QmmPr
           float val = v[k];
           if constexpr (NB == 2) {
             const float g = round_to(v[k], yd), up = round_to(u[k], yd);
-            val = g / (1.0f + expf(-g)) * up;
+            val = jqk::glu_value(g, up, p.glu_limit, p.glu_scale ? p.glu_scale[orow] : 1.f);
           }
           store_out(p.y, orow * N + n0 + lr, val, yd);
         }

@@ -540,6 +540,11 @@ struct Dmx {
         if constexpr (GATHER) {
           const int64_t N = wc.N;
           const int64_t n = row0 + TSTEP * rr + lr;
+          int64_t orow = tk.orow[0];
+          bool live = tk.olive[0];
+#pragma unroll
+          for (int q = 1; q < TPL; ++q)
+            if (k == q) orow = tk.orow[q], live = tk.olive[q];
           if constexpr (NB == 2) {
             float u = 0.f;
             const int slot1 = (ab * RT + 1) * TPL + k;
@@ -547,13 +552,10 @@ struct Dmx {
             for (int w = 0; w < kMaxKW; ++w)
               if (w < KW) u += red[((par * KW + w) * NOUT + slot1) * 64 + lane];
             const float gg = round_to(v, a.yd), uu = round_to(u, a.yd);
-            v = gg / (1.0f + expf(-gg)) * uu;
+            const jqk::QmmProblem& gp = a.g[0];
+            v = jqk::glu_value(gg, uu, gp.glu_limit,
+                               gp.glu_scale && live ? gp.glu_scale[orow] : 1.f);
           }
-          int64_t orow = tk.orow[0];
-          bool live = tk.olive[0];
-#pragma unroll
-          for (int q = 1; q < TPL; ++q)
-            if (k == q) orow = tk.orow[q], live = tk.olive[q];
           if (live && n < N) store_out(a.g[0].y, orow * N + n, v, a.yd);
         } else {
           const int64_t n = row0 + 16 * rr + lr;

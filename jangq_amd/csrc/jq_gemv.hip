@@ -45,6 +45,7 @@ struct GemvArgs {
   int ushift;    // log2(gs / 32)
   int kwshift;   // log2(waves per block)
   int yd;
+  float glu_limit;  // SwiGLU clamp (gemv_row_kernel GLU form), 0: none
 };
 
 // Persistent: block b handles row blocks b, b + gridDim.x, ... Each lane keeps a rolling
@@ -335,7 +336,7 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a) {
         const bool bf = a.yd == JQ_BF16;
         const float g = bf ? bf16_bits_to_f32(f32_to_bf16_bits(gt)) : f16_bits_to_f32(f32_to_f16_bits(gt));
         const float u = bf ? bf16_bits_to_f32(f32_to_bf16_bits(ut)) : f16_bits_to_f32(f32_to_f16_bits(ut));
-        const float hv = g / (1.0f + expf(-g)) * u;
+        const float hv = jqk::glu_value(g, u, a.glu_limit, 1.f);
         if (bf) store_t<JQ_BF16>(pb.y, row0, hv);
         else store_t<JQ_F16>(pb.y, row0, hv);
       }
@@ -514,6 +515,7 @@ int gemv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, 
   a.nprob = nprob;
   a.ushift = gs == 32 ? 0 : gs == 64 ? 1 : 2;
   a.yd = yd;
+  a.glu_limit = 0.f;
   switch (bits) {
     case 2: return launch_x<2>(a, xd, sb, st);
     case 3: return launch_x<3>(a, xd, sb, st);
@@ -529,7 +531,7 @@ bool gemv_swiglu_ok(int M, int64_t K, int64_t N, int bits, int gs, int xd, int s
          gemv_waves(K, bits, nullptr) <= 2;
 }
 
-int gemv_swiglu_launch(const QmvBatch& b, int bits, int gs, int xd, int sb, int yd,
+int gemv_swiglu_launch(const QmvBatch& b, int bits, int gs, int xd, int sb, int yd, float limit,
                        hipStream_t st) {
   if (b.p[0].N == 0) return JQ_OK;
   if (!gemv_swiglu_ok(b.M, b.K, b.p[0].N, bits, gs, xd, sb, yd) || b.p[1].N != b.p[0].N ||
@@ -540,6 +542,7 @@ int gemv_swiglu_launch(const QmvBatch& b, int bits, int gs, int xd, int sb, int 
   a.nprob = 2;
   a.ushift = gs == 32 ? 0 : gs == 64 ? 1 : 2;
   a.yd = yd;
+  a.glu_limit = limit;
 #define JQ_GLU(B)                                                     \
   if (xd == JQ_BF16) return launch_glu_sb<B, JQ_BF16>(a, sb, st);     \
   return launch_glu_sb<B, JQ_F16>(a, sb, st);

@@ -42,22 +42,42 @@ struct GatherArgs {
   int ushift;       // log2(gs / 32)
   int kwshift;      // log2(waves per block)
   int yd;
-  // Combined form (direct pairs t*ck + j, one row each): out[t, n] = round(sum_j cw[t*ck+j] *
-  // y[t*ck+j, n]) (+ cshared[t, n]), the k experts of a token summed in slot order.
+  // Combined form (direct pairs t*ck + j, one row each): the k experts of a token summed in
+  // slot order, then the shared expert's term (jqk::moe_final):
+  //   after the down projection (cbefore = 0): round(sum_j cw[t*ck+j] * y[t*ck+j, n])
+  //   before it (cbefore = 1, weights already in h):   sum_j y[t*ck+j, n]
+  // with each slot output y rounded to the output dtype first.
   const float* cw;
   const void* cshared;
+  const void* cgate;  // [T] logits of the shared term's sigmoid gate, or NULL
   void* cout;
-  int ck, ctok;
+  int ck, ctok, cbefore;
   // Routed form (direct pairs t*rk + j of a launch that routes for itself): pair t*rk + j
-  // uses the j-th expert of top-rk(softmax(rlogits[t])); the token's ids and weights go to
-  // ridx / rw (for the launches that follow).
-  const float* rlogits;
+  // uses the j-th expert of the token's top-rk (jqr::route_wave on rlogits[t]); the token's
+  // ids and weights go to ridx / rw (for the launches that follow). With rbefore, h of pair
+  // t*rk + j is multiplied by its routing weight.
+  const void* rlogits;
   uint32_t* ridx;
   float* rw;
-  int rE, rk, rrenorm;
+  int rE, rk, rbefore;
+  jqr::RouteOpts ro;
 };
 
 constexpr int kRouteSlots = 8;  // routed form: up to 64 * 8 = 512 experts
+
+// No combined or routed form.
+void init_forms(GatherArgs& a) {
+  a.cw = nullptr;
+  a.cshared = nullptr;
+  a.cgate = nullptr;
+  a.cout = nullptr;
+  a.ck = a.ctok = a.cbefore = 0;
+  a.rlogits = nullptr;
+  a.ridx = nullptr;
+  a.rw = nullptr;
+  a.rE = a.rk = a.rbefore = 0;
+  a.ro = jqr::softmax_opts(1);
+}
 
 JQ_DEV float round_out(float v, int yd) {
   if (yd == JQ_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
@@ -247,8 +267,9 @@ gemv_gather_kernel(GatherArgs a) {
     if constexpr (ROUTE) {
       const int tok = t / a.rk, j = t - tok * a.rk;
       if (tok != rt_tok) {  // wave-uniform
-        jqr::route_wave<kRouteSlots>(a.rlogits + (int64_t)tok * a.rE, a.rE, a.rk, a.rrenorm,
-                                     lane, rt_id, rt_w);
+        jqr::route_wave<kRouteSlots>(
+            (const char*)a.rlogits + (int64_t)tok * a.rE * (a.ro.logit_dtype == JQ_F32 ? 4 : 2),
+            a.rE, a.rk, a.ro, lane, rt_id, rt_w);
         rt_tok = tok;
       }
       const uint32_t e = (uint32_t)__builtin_amdgcn_readlane((int)rt_id, j);
@@ -330,15 +351,20 @@ gemv_gather_kernel(GatherArgs a) {
     __syncthreads();
     if constexpr (COMB) {
       // Each slot's output row, rounded as the expert output, joins the token's sum in slot
-      // order (fp32); then round, + shared, store.
+      // order (fp32); then the shared expert's term, and the store rounds.
       const int64_t row = row0 + lane;
       if (wave == 0 && lane < ROWS && row < N) {
         float comb = 0.f;
-        for (int j = 0; j < a.ck; ++j)
-          comb = fmaf(a.cw[ct * a.ck + j], round_out(red[par][j][lane], a.yd), comb);
-        float r = round_out(comb, a.yd);
-        if (a.cshared) r += load_out(a.cshared, (int64_t)ct * N + row, a.yd);
-        store_out(a.cout, (int64_t)ct * N + row, r, a.yd);
+        for (int j = 0; j < a.ck; ++j) {
+          const float y = round_out(red[par][j][lane], a.yd);
+          comb = a.cbefore ? comb + y : fmaf(a.cw[ct * a.ck + j], y, comb);
+        }
+        const float sh = a.cshared ? load_out(a.cshared, (int64_t)ct * N + row, a.yd) : 0.f;
+        const float gl = a.cgate ? load_out(a.cgate, ct, a.yd) : 0.f;
+        store_out(a.cout, (int64_t)ct * N + row,
+                  jqk::moe_final(a.cbefore, comb, a.cshared != nullptr, sh, a.cgate != nullptr, gl,
+                                 a.yd),
+                  a.yd);
       }
     } else if (wave == 0 && lane < ROWS * MT) {
       const int j = lane / MT, m = lane % MT;
@@ -355,7 +381,13 @@ gemv_gather_kernel(GatherArgs a) {
           float u = 0.f;
           for (int w = 0; w < KW; ++w) u += red[par][w][(NB * j + 1) * MT + m];
           const float g = round_out(v, a.yd), up = round_out(u, a.yd);
-          v = g / (1.0f + expf(-g)) * up;
+          // the pair's routing weight when it enters before the down projection
+          float f = a.p[0].glu_scale ? a.p[0].glu_scale[orow] : 1.f;
+          if constexpr (ROUTE) {
+            const int jj = tile - (tile / a.rk) * a.rk;
+            f = a.rbefore ? jqr::lane_read(rt_w, jj) : 1.f;
+          }
+          v = jqk::glu_value(g, up, a.p[0].glu_limit, f);
         }
         store_out(a.p[0].y, orow * N + row, v, a.yd);
       }
@@ -493,14 +525,7 @@ int gemv_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPl
   a.plan = plan;
   a.ushift = gs == 32 ? 0 : gs == 64 ? 1 : 2;
   a.yd = yd;
-  a.cw = nullptr;
-  a.cshared = nullptr;
-  a.cout = nullptr;
-  a.ck = a.ctok = 0;
-  a.rlogits = nullptr;
-  a.ridx = nullptr;
-  a.rw = nullptr;
-  a.rE = a.rk = a.rrenorm = 0;
+  init_forms(a);
   if (p2) return launch_bits<2>(a, bits, xd, sb, tile_rows, max_tiles, st);
   return launch_bits<1>(a, bits, xd, sb, tile_rows, max_tiles, st);
 }
@@ -514,27 +539,26 @@ bool gemv_gather_comb_ok(int64_t T, int k, int64_t N, int64_t K, int bits, int g
          (C <= 32 || gemv_waves(K, bits, nullptr) == 1) && T * k < ((int64_t)1 << 20);
 }
 
-int gemv_gather_comb_launch(const QmmProblem& p, const GatherPlan& plan, const float* w,
-                            const void* shared, void* out, int64_t T, int k, int bits, int gs,
-                            int xd, int sb, int yd, hipStream_t st) {
+int gemv_gather_comb_launch(const QmmProblem& p, const GatherPlan& plan, const MoeCombine& c,
+                            int64_t T, int k, int bits, int gs, int xd, int sb, int yd,
+                            hipStream_t st) {
   if (T == 0 || p.N == 0) return JQ_OK;
   if (!gemv_gather_comb_ok(T, k, p.N, p.K, bits, gs, xd, sb) || plan.tiles || plan.lhs ||
-      plan.direct_rows != 1 || plan.direct_pairs != T * k || !w || !out)
+      plan.direct_rows != 1 || plan.direct_pairs != T * k || (!c.w && !c.before) || !c.out)
     return JQ_ERR_SHAPE;
   GatherArgs a;
   a.p[0] = a.p[1] = p;
   a.plan = plan;
   a.ushift = gs == 32 ? 0 : gs == 64 ? 1 : 2;
   a.yd = yd;
-  a.cw = w;
-  a.cshared = shared;
-  a.cout = out;
+  init_forms(a);
+  a.cw = c.w;
+  a.cshared = c.shared;
+  a.cgate = c.shared_gate;
+  a.cout = c.out;
+  a.cbefore = c.before;
   a.ck = k;
   a.ctok = (int)T;
-  a.rlogits = nullptr;
-  a.ridx = nullptr;
-  a.rw = nullptr;
-  a.rE = a.rk = a.rrenorm = 0;
   return launch_bits<1>(a, bits, xd, sb, 1, T * k, st);
 }
 
@@ -543,9 +567,9 @@ bool gemv_gather_route_ok(int64_t E, int k) {
 }
 
 int gemv_gather_route_launch(const QmmProblem& g, const QmmProblem& u, const GatherPlan& plan,
-                             const float* logits, int64_t E, int k, int renorm, uint32_t* idx,
-                             float* w, int64_t T, int bits, int gs, int xd, int sb, int yd,
-                             hipStream_t st) {
+                             const void* logits, int64_t E, int k, const jqr::RouteOpts& ro,
+                             int before, uint32_t* idx, float* w, int64_t T, int bits, int gs,
+                             int xd, int sb, int yd, hipStream_t st) {
   if (T == 0 || g.N == 0) return JQ_OK;
   if (!gemv_gather_route_ok(E, k) || !gemv_gather_ok(g.N, g.K, bits, gs, xd, sb) ||
       plan.tiles || plan.lhs || plan.direct_rows != 1 || plan.direct_pairs != T * k ||
@@ -557,16 +581,14 @@ int gemv_gather_route_launch(const QmmProblem& g, const QmmProblem& u, const Gat
   a.plan = plan;
   a.ushift = gs == 32 ? 0 : gs == 64 ? 1 : 2;
   a.yd = yd;
-  a.cw = nullptr;
-  a.cshared = nullptr;
-  a.cout = nullptr;
-  a.ck = a.ctok = 0;
+  init_forms(a);
   a.rlogits = logits;
   a.ridx = idx;
   a.rw = w;
   a.rE = (int)E;
   a.rk = k;
-  a.rrenorm = renorm;
+  a.rbefore = before;
+  a.ro = ro;
   return launch_bits<2>(a, bits, xd, sb, 1, T * k, st);
 }
 

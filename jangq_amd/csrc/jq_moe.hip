@@ -29,15 +29,17 @@ constexpr int kMaxExperts = 4096;
 
 // One wave per token (jqr::route_wave).
 template <int SL>
-__global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ logits, int T, int E,
-                                                    int k, int renorm, uint32_t* __restrict__ idx,
+__global__ void __launch_bounds__(256) route_kernel(const void* __restrict__ logits, int T, int E,
+                                                    int k, jqr::RouteOpts o,
+                                                    uint32_t* __restrict__ idx,
                                                     float* __restrict__ wout) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   uint32_t id;
   float w;
-  jqr::route_wave<SL>(logits + (int64_t)t * E, E, k, renorm, lane, id, w);
+  const int esz = o.logit_dtype == JQ_F32 ? 4 : 2;
+  jqr::route_wave<SL>((const char*)logits + (int64_t)t * E * esz, E, k, o, lane, id, w);
   if (lane < k) {
     idx[(int64_t)t * k + lane] = id;
     wout[(int64_t)t * k + lane] = w;
@@ -264,49 +266,47 @@ int check_expert_shape(int bits, int gs, int64_t E, int64_t N, int64_t K) {
   return JQ_OK;
 }
 
-// out[t, i] = round(sum_j w[t, j] * y[t, j, i]) (fp32, slot order), then round(+ shared[t, i]).
+// The MoE combine (jqk::MoeCombine) of y [T, k, H] (slot outputs already rounded).
 // One thread per 8 consecutive elements of a row (H % 8 == 0) or per element.
 template <int DT, int VEC>
 __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ y,
-                                                      const float* __restrict__ w,
-                                                      const void* __restrict__ shared, int64_t T,
-                                                      int k, int64_t H, void* __restrict__ out) {
+                                                      jqk::MoeCombine c, int64_t T, int k,
+                                                      int64_t H) {
   const int64_t per_row = H / VEC;
   const int64_t n = T * per_row;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t t = i / per_row, c = (i - t * per_row) * VEC;
+    const int64_t t = i / per_row, col = (i - t * per_row) * VEC;
     float acc[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) acc[v] = 0.f;
     for (int j = 0; j < k; ++j) {
-      const float wj = w[t * k + j];
-      const int64_t base = (t * k + j) * H + c;
+      const float wj = c.before ? 1.f : c.w[t * k + j];
+      const int64_t base = (t * k + j) * H + col;
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[v] = fmaf(wj, load_t<DT>(y, base + v), acc[v]);
+      for (int v = 0; v < VEC; ++v)
+        acc[v] = c.before ? acc[v] + load_t<DT>(y, base + v) : fmaf(wj, load_t<DT>(y, base + v), acc[v]);
     }
+    const float gl = c.shared_gate ? load_t<DT>(c.shared_gate, t) : 0.f;
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      float r = acc[v];
-      if constexpr (DT != JQ_F32) {
-        r = DT == JQ_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(r))
-                          : f16_bits_to_f32(f32_to_f16_bits(r));
-      }
-      if (shared) r += load_t<DT>(shared, t * H + c + v);
-      store_t<DT>(out, t * H + c + v, r);
+      const float sh = c.shared ? load_t<DT>(c.shared, t * H + col + v) : 0.f;
+      store_t<DT>(c.out, t * H + col + v,
+                  jqk::moe_final(c.before, acc[v], c.shared != nullptr, sh,
+                                 c.shared_gate != nullptr, gl, DT));
     }
   }
 }
 
-// h = round(silu(g) * u) elementwise (g, u already rounded to the output dtype).
+// h = round(silu(g) * u) elementwise (g, u already rounded to the output dtype), with the
+// optional clamp.
 template <int DT>
 __global__ void __launch_bounds__(256) swiglu_kernel(const void* __restrict__ g,
                                                      const void* __restrict__ u, int64_t n,
-                                                     void* __restrict__ h) {
+                                                     float limit, void* __restrict__ h) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const float gv = load_t<DT>(g, i), uv = load_t<DT>(u, i);
-    store_t<DT>(h, i, gv / (1.0f + expf(-gv)) * uv);
+    store_t<DT>(h, i, jqk::glu_value(load_t<DT>(g, i), load_t<DT>(u, i), limit, 1.f));
   }
 }
 
@@ -315,22 +315,50 @@ inline unsigned grid_for(int64_t n) {
   return (unsigned)(b < 8192 ? (b < 1 ? 1 : b) : 8192);
 }
 
+// Routing options from the C ABI (NULL: softmax with renormalisation, the qwen-style router).
+int route_opts_of(const jq_route_opts* p, int64_t E, jqr::RouteOpts& o) {
+  o = jqr::softmax_opts(1);
+  if (!p) return JQ_OK;
+  if (p->score < JQ_SCORE_SOFTMAX || p->score > JQ_SCORE_SQRTSOFTPLUS) return JQ_ERR_SHAPE;
+  if (!(p->renorm_eps >= 0.f) || !isfinite(p->renorm_eps) || !isfinite(p->scaling))
+    return JQ_ERR_SHAPE;
+  const int ng = p->n_group < 1 ? 1 : p->n_group;
+  if (ng > 1) {
+    if (ng > 64 || E % ng || p->topk_group < 1 || p->topk_group > ng) return JQ_ERR_SHAPE;
+  }
+  o.score = p->score;
+  o.renorm = p->renorm ? 1 : 0;
+  o.eps = p->renorm_eps;
+  o.scale = p->scaling;
+  o.bias = p->score_bias;
+  o.n_group = ng;
+  o.topk_group = ng > 1 ? p->topk_group : 1;
+  return JQ_OK;
+}
+
+jq_route_opts softmax_route_opts(int renorm) {
+  jq_route_opts o;
+  o.score = JQ_SCORE_SOFTMAX;
+  o.renorm = renorm;
+  o.renorm_eps = 0.f;
+  o.scaling = 1.f;
+  o.score_bias = nullptr;
+  o.n_group = 1;
+  o.topk_group = 1;
+  return o;
+}
+
 }  // namespace
 
 extern "C" {
 
-int jq_moe_combine(const void* y, const float* w, const void* shared, int64_t T, int k,
-                   int64_t H, void* out, int dtype, jq_stream_t stream) {
-  if (T < 0 || k <= 0 || H < 0) return JQ_ERR_SHAPE;
-  if (!jqh::dtype_ok(dtype)) return JQ_ERR_DTYPE;
-  if (T == 0 || H == 0) return JQ_OK;
-  if (!y || !w || !out) return JQ_ERR_NULL;
-  hipStream_t st = (hipStream_t)stream;
+static int combine_launch(const void* y, const jqk::MoeCombine& c, int64_t T, int k, int64_t H,
+                          int dtype, hipStream_t st) {
   const bool vec = H % 8 == 0;
   const int64_t n = T * (vec ? H / 8 : H);
-#define JQ_C(DT)                                                                             \
-  if (vec) combine_kernel<DT, 8><<<grid_for(n), 256, 0, st>>>(y, w, shared, T, k, H, out);  \
-  else combine_kernel<DT, 1><<<grid_for(n), 256, 0, st>>>(y, w, shared, T, k, H, out);
+#define JQ_C(DT)                                                                  \
+  if (vec) combine_kernel<DT, 8><<<grid_for(n), 256, 0, st>>>(y, c, T, k, H);    \
+  else combine_kernel<DT, 1><<<grid_for(n), 256, 0, st>>>(y, c, T, k, H);
   if (dtype == JQ_BF16) { JQ_C(JQ_BF16) }
   else if (dtype == JQ_F16) { JQ_C(JQ_F16) }
   else { JQ_C(JQ_F32) }
@@ -338,21 +366,36 @@ int jq_moe_combine(const void* y, const float* w, const void* shared, int64_t T,
   return jqh::launch_status();
 }
 
-int jq_quantized_swiglu(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
-                        const uint32_t* gate_codes, const void* gate_scales,
-                        const void* gate_biases, const uint32_t* up_codes, const void* up_scales,
-                        const void* up_biases, int sb_dtype, int bits, int group_size, void* h,
-                        void* up_buf, int y_dtype, jq_stream_t stream) {
+int jq_moe_combine(const void* y, const float* w, const void* shared, int64_t T, int k,
+                   int64_t H, void* out, int dtype, jq_stream_t stream) {
+  if (T < 0 || k <= 0 || H < 0) return JQ_ERR_SHAPE;
+  if (!jqh::dtype_ok(dtype)) return JQ_ERR_DTYPE;
+  if (T == 0 || H == 0) return JQ_OK;
+  if (!y || !w || !out) return JQ_ERR_NULL;
+  jqk::MoeCombine c;
+  c.w = w;
+  c.shared = shared;
+  c.shared_gate = nullptr;
+  c.out = out;
+  c.before = 0;
+  return combine_launch(y, c, T, k, H, dtype, (hipStream_t)stream);
+}
+
+static int swiglu_run(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
+                      const uint32_t* gate_codes, const void* gate_scales, const void* gate_biases,
+                      const uint32_t* up_codes, const void* up_scales, const void* up_biases,
+                      int sb_dtype, int bits, int group_size, void* h, void* up_buf, int y_dtype,
+                      float limit, hipStream_t st) {
   int s = jqh::check_qshape(bits, group_size, N, K);
   if (s) return s;
   if (M < 0 || M > ((int64_t)1 << 30)) return JQ_ERR_SHAPE;
   if (!jqh::dtype_ok(x_dtype) || !jqh::dtype_ok(sb_dtype) || !jqh::dtype_ok(y_dtype))
     return JQ_ERR_DTYPE;
+  if (!(limit >= 0.f)) return JQ_ERR_SHAPE;
   if (M == 0 || N == 0) return JQ_OK;
   if (!x || !gate_codes || !gate_scales || !gate_biases || !up_codes || !up_scales ||
       !up_biases || !h)
     return JQ_ERR_NULL;
-  hipStream_t st = (hipStream_t)stream;
   // One activation row: the whole-rows-per-wave GEMV with the SiLU * up epilogue.
   if (jqk::gemv_swiglu_ok((int)M, K, N, bits, group_size, x_dtype, sb_dtype, y_dtype)) {
     jqk::QmvBatch b;
@@ -362,7 +405,7 @@ int jq_quantized_swiglu(const void* x, int x_dtype, int64_t M, int64_t N, int64_
     b.p[0].biases = gate_biases; b.p[0].y = h; b.p[0].N = N;
     b.p[1] = b.p[0];
     b.p[1].codes = up_codes; b.p[1].scales = up_scales; b.p[1].biases = up_biases;
-    return jqk::gemv_swiglu_launch(b, bits, group_size, x_dtype, sb_dtype, y_dtype, st);
+    return jqk::gemv_swiglu_launch(b, bits, group_size, x_dtype, sb_dtype, y_dtype, limit, st);
   }
   // Decode sizes: one grouped launch of the expert-gathered GEMV over a single "expert" whose
   // tile holds all M rows, with the SiLU * up epilogue.
@@ -377,6 +420,7 @@ int jq_quantized_swiglu(const void* x, int x_dtype, int64_t M, int64_t N, int64_
     g.M = 1; g.N = N; g.K = K;
     g.expert_stride_codes = 0;
     g.expert_stride_sb = 0;
+    g.glu_limit = limit;
     u = g;
     u.codes = up_codes; u.scales = up_scales; u.biases = up_biases;
     const int tr = M <= 1 ? 1 : M <= 2 ? 2 : 4;
@@ -393,25 +437,51 @@ int jq_quantized_swiglu(const void* x, int x_dtype, int64_t M, int64_t N, int64_
   const int64_t Mv[2] = {M, M}, Nv[2] = {N, N}, Kv[2] = {K, K};
   void* ys[2] = {h, up_buf};
   s = jq_quantized_matmul_multi(2, xs, x_dtype, cs, ss, bs, sb_dtype, bv, gv, Mv, Nv, Kv, ys,
-                                y_dtype, stream);
+                                y_dtype, (jq_stream_t)st);
   if (s) return s;
   const int64_t n = M * N;
-  if (y_dtype == JQ_BF16) swiglu_kernel<JQ_BF16><<<grid_for(n), 256, 0, st>>>(h, up_buf, n, h);
-  else if (y_dtype == JQ_F16) swiglu_kernel<JQ_F16><<<grid_for(n), 256, 0, st>>>(h, up_buf, n, h);
-  else swiglu_kernel<JQ_F32><<<grid_for(n), 256, 0, st>>>(h, up_buf, n, h);
+  if (y_dtype == JQ_BF16) swiglu_kernel<JQ_BF16><<<grid_for(n), 256, 0, st>>>(h, up_buf, n, limit, h);
+  else if (y_dtype == JQ_F16) swiglu_kernel<JQ_F16><<<grid_for(n), 256, 0, st>>>(h, up_buf, n, limit, h);
+  else swiglu_kernel<JQ_F32><<<grid_for(n), 256, 0, st>>>(h, up_buf, n, limit, h);
   return jqh::launch_status();
 }
 
+int jq_quantized_swiglu(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
+                        const uint32_t* gate_codes, const void* gate_scales,
+                        const void* gate_biases, const uint32_t* up_codes, const void* up_scales,
+                        const void* up_biases, int sb_dtype, int bits, int group_size, void* h,
+                        void* up_buf, int y_dtype, jq_stream_t stream) {
+  return swiglu_run(x, x_dtype, M, N, K, gate_codes, gate_scales, gate_biases, up_codes,
+                    up_scales, up_biases, sb_dtype, bits, group_size, h, up_buf, y_dtype, 0.f,
+                    (hipStream_t)stream);
+}
 
-int jq_moe_route(const float* logits, int64_t T, int64_t E, int k, int renorm, uint32_t* idx,
-                 float* weights, jq_stream_t stream) {
+int jq_quantized_swiglu_ex(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
+                           const uint32_t* gate_codes, const void* gate_scales,
+                           const void* gate_biases, const uint32_t* up_codes,
+                           const void* up_scales, const void* up_biases, int sb_dtype, int bits,
+                           int group_size, float swiglu_limit, void* h, void* up_buf,
+                           int y_dtype, jq_stream_t stream) {
+  return swiglu_run(x, x_dtype, M, N, K, gate_codes, gate_scales, gate_biases, up_codes,
+                    up_scales, up_biases, sb_dtype, bits, group_size, h, up_buf, y_dtype,
+                    swiglu_limit, (hipStream_t)stream);
+}
+
+
+int jq_moe_route_ex(const void* logits, int logits_dtype, int64_t T, int64_t E, int k,
+                    const jq_route_opts* opts, uint32_t* idx, float* weights, jq_stream_t stream) {
   if (T < 0 || E <= 0 || E > kMaxExperts || k <= 0 || k > E || k > 64) return JQ_ERR_SHAPE;
+  if (!jqh::dtype_ok(logits_dtype)) return JQ_ERR_DTYPE;
+  jqr::RouteOpts o;
+  int s = route_opts_of(opts, E, o);
+  if (s) return s;
+  o.logit_dtype = logits_dtype;
   if (T == 0) return JQ_OK;
   if (!logits || !idx || !weights) return JQ_ERR_NULL;
   const unsigned grid = (unsigned)((T + 3) / 4);
   hipStream_t st = (hipStream_t)stream;
   const int sl = (int)((E + 63) / 64);
-#define JQ_R(SL) route_kernel<SL><<<grid, 256, 0, st>>>(logits, (int)T, (int)E, k, renorm, idx, weights)
+#define JQ_R(SL) route_kernel<SL><<<grid, 256, 0, st>>>(logits, (int)T, (int)E, k, o, idx, weights)
   if (sl <= 1) JQ_R(1);
   else if (sl <= 2) JQ_R(2);
   else if (sl <= 4) JQ_R(4);
@@ -421,6 +491,12 @@ int jq_moe_route(const float* logits, int64_t T, int64_t E, int k, int renorm, u
   else JQ_R(64);
 #undef JQ_R
   return jqh::launch_status();
+}
+
+int jq_moe_route(const float* logits, int64_t T, int64_t E, int k, int renorm, uint32_t* idx,
+                 float* weights, jq_stream_t stream) {
+  const jq_route_opts o = softmax_route_opts(renorm);
+  return jq_moe_route_ex(logits, JQ_F32, T, E, k, &o, idx, weights, stream);
 }
 
 int64_t jq_gather_workspace_size(int64_t n_pairs, int64_t E, int64_t M) {
@@ -473,54 +549,84 @@ int jq_gather_qmm(const void* x, int x_dtype, int64_t x_batch, int64_t M, const 
   return grouped_launch(c, p, nullptr, plan, mt, bits, group_size, x_dtype, sb_dtype, y_dtype, st);
 }
 
-// jq_switch_glu, and with comb_out != NULL the combine of jq_moe_combine fused into the down
-// launch where the direct decode form applies (else out is written and combined after).
-static int switch_glu_run(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
-                          int64_t E, const uint32_t* idx, int k, const uint32_t* gate_codes,
-                          const void* gate_scales, const void* gate_biases,
-                          const uint32_t* up_codes, const void* up_scales, const void* up_biases,
-                          int bits_gu, const uint32_t* down_codes, const void* down_scales,
-                          const void* down_biases, int bits_d, int sb_dtype, int group_size,
-                          void* h_buf, void* out, int y_dtype, void* workspace,
-                          int64_t workspace_bytes, const float* cw, const void* cshared,
-                          void* comb_out, hipStream_t st, const float* rlogits = nullptr,
-                          int renorm = 1) {
-  int s = check_expert_shape(bits_gu, group_size, E, I, H);
+}  // extern "C"
+
+namespace {
+
+// One routed-expert call (jq_switch_glu, jq_switch_glu_combine, jq_moe_experts, jq_moe_block).
+struct MoeRun {
+  const void* x;
+  int xd, yd, sb, gs, bits_gu, bits_d, k;
+  int64_t T, H, I, E;
+  const uint32_t* idx;  // [T, k] expert ids (written here when logits are given)
+  const float* cw;      // [T, k] routing weights (likewise)
+  const void* logits;   // [T, E] router logits (dtype ro.logit_dtype), or NULL (ids given)
+  jqr::RouteOpts ro;
+  const uint32_t *gc, *uc, *dc;
+  const void *gsc, *gb, *usc, *ub, *dsc, *db;
+  float limit;   // SwiGLU clamp
+  int before;    // routing weights enter h before the down projection
+  void* h_buf;   // [T*k, I]
+  void* y_buf;   // [T*k, H] slot outputs (the jq_switch_glu output when comb.out is NULL)
+  jqk::MoeCombine comb;  // comb.out NULL: no combine (jq_switch_glu)
+  void* workspace;
+  int64_t workspace_bytes;
+};
+
+int moe_run(MoeRun& r, hipStream_t st) {
+  int s = check_expert_shape(r.bits_gu, r.gs, r.E, r.I, r.H);
   if (s) return s;
-  s = check_expert_shape(bits_d, group_size, E, H, I);
+  s = check_expert_shape(r.bits_d, r.gs, r.E, r.H, r.I);
   if (s) return s;
-  if (x_dtype != JQ_BF16 && x_dtype != JQ_F16) return JQ_ERR_DTYPE;
-  if (!jqh::dtype_ok(sb_dtype) || (y_dtype != JQ_BF16 && y_dtype != JQ_F16)) return JQ_ERR_DTYPE;
-  if (y_dtype != x_dtype) return JQ_ERR_DTYPE;  // h feeds the down projection as activations
-  if (T < 0 || k <= 0) return JQ_ERR_SHAPE;
-  if (H % 128 || I % 128) return JQ_ERR_SHAPE;
-  const int64_t n_pairs = T * k;
+  if (r.xd != JQ_BF16 && r.xd != JQ_F16) return JQ_ERR_DTYPE;
+  if (!jqh::dtype_ok(r.sb) || (r.yd != JQ_BF16 && r.yd != JQ_F16)) return JQ_ERR_DTYPE;
+  if (r.yd != r.xd) return JQ_ERR_DTYPE;  // h feeds the down projection as activations
+  if (r.T < 0 || r.k <= 0) return JQ_ERR_SHAPE;
+  if (r.H % 128 || r.I % 128) return JQ_ERR_SHAPE;
+  if (!(r.limit >= 0.f)) return JQ_ERR_SHAPE;
+  const int64_t n_pairs = r.T * r.k;
   if (n_pairs == 0) return JQ_OK;
-  if (!x || !idx || !gate_codes || !gate_scales || !gate_biases || !up_codes || !up_scales ||
-      !up_biases || !down_codes || !down_scales || !down_biases || !h_buf || !out)
+  if (!r.x || !r.idx || !r.gc || !r.gsc || !r.gb || !r.uc || !r.usc || !r.ub || !r.dc ||
+      !r.dsc || !r.db || !r.h_buf || !r.y_buf)
     return JQ_ERR_NULL;
-  if (comb_out && !cw) return JQ_ERR_NULL;
-  if (!workspace || workspace_bytes < ws_layout(n_pairs, E, 1).total) return JQ_ERR_WORKSPACE;
+  if (r.comb.out && !r.cw) return JQ_ERR_NULL;
+  if (r.before && !r.cw) return JQ_ERR_NULL;
+  if (!r.workspace || r.workspace_bytes < ws_layout(n_pairs, r.E, 1).total) return JQ_ERR_WORKSPACE;
+  const int64_t T = r.T, H = r.H, I = r.I, E = r.E;
+  const int k = r.k;
   // With logits, idx and cw are outputs: the routing of the T tokens.
   // Pair i = t*k + j uses x row t = i / k and expert idx[i]; one plan serves both launches
   // (gate+up reads x rows i / k, down reads h rows i).
-  const int bv[2] = {bits_gu, bits_d};
+  const int bv[2] = {r.bits_gu, r.bits_d};
   const int64_t Nv[2] = {I, H}, Kv[2] = {H, I};
-  const Choice c = choose(n_pairs, E, n_pairs, group_size, x_dtype, sb_dtype, 2, bv, Nv, Kv);
+  const Choice c = choose(n_pairs, E, n_pairs, r.gs, r.xd, r.sb, 2, bv, Nv, Kv);
   jqk::GatherPlan plan;
   const bool direct = c.k == Kern::gemv && c.tile_rows == 1;
+  const bool comb_fused = r.comb.out && direct &&
+                          jqk::gemv_gather_comb_ok(T, k, H, I, r.bits_d, r.gs, r.yd, r.sb);
   // Routing inside the gate|up launch: decode sizes with the combine fused into the down
   // launch, so that the three MoE launches after the router become two.
-  const bool self_route = rlogits && direct && comb_out && jqk::gemv_gather_route_ok(E, k) &&
-                          jqk::gemv_gather_comb_ok(T, k, H, I, bits_d, group_size, y_dtype, sb_dtype);
-  if (rlogits && !self_route) {
-    s = jq_moe_route(rlogits, T, E, k, renorm, (uint32_t*)idx, (float*)cw, (jq_stream_t)st);
+  const bool self_route = r.logits && comb_fused && jqk::gemv_gather_route_ok(E, k);
+  if (r.logits && !self_route) {
+    if (E > kMaxExperts || k > E || k > 64) return JQ_ERR_SHAPE;
+    const int sl = (int)((E + 63) / 64);
+    const unsigned grid = (unsigned)((T + 3) / 4);
+#define JQ_R(SL) route_kernel<SL><<<grid, 256, 0, st>>>(r.logits, (int)T, (int)E, k, r.ro, (uint32_t*)r.idx, (float*)r.cw)
+    if (sl <= 1) JQ_R(1);
+    else if (sl <= 2) JQ_R(2);
+    else if (sl <= 4) JQ_R(4);
+    else if (sl <= 8) JQ_R(8);
+    else if (sl <= 16) JQ_R(16);
+    else if (sl <= 32) JQ_R(32);
+    else JQ_R(64);
+#undef JQ_R
+    s = jqh::launch_status();
     if (s) return s;
   }
   if (direct) {
-    plan = direct_plan(idx, n_pairs, E, nullptr);
+    plan = direct_plan(r.idx, n_pairs, E, nullptr);
   } else {
-    s = build_plan(idx, n_pairs, E, 1, c.tile_rows, workspace, plan, nullptr, st);
+    s = build_plan(r.idx, n_pairs, E, 1, c.tile_rows, r.workspace, plan, nullptr, st);
     if (s) return s;
   }
   jqk::GatherPlan plan_gu = plan;
@@ -529,32 +635,89 @@ static int switch_glu_run(const void* x, int x_dtype, int64_t T, int64_t H, int6
   plan_gu.x_rows = T;
   plan.x_rows = n_pairs;  // down reads h rows = pairs
   jqk::QmmProblem g, u, d;
-  g.x = x; g.codes = gate_codes; g.scales = gate_scales; g.biases = gate_biases; g.y = h_buf;
+  g.x = r.x; g.codes = r.gc; g.scales = r.gsc; g.biases = r.gb; g.y = r.h_buf;
   g.M = 1; g.N = I; g.K = H;
-  g.expert_stride_codes = I * (H * bits_gu / 32);
-  g.expert_stride_sb = I * (H / group_size);
+  g.expert_stride_codes = I * (H * r.bits_gu / 32);
+  g.expert_stride_sb = I * (H / r.gs);
+  g.glu_limit = r.limit;
+  // the pair weights enter h (weights before the down projection): from the routing output,
+  // or from the registers of the launch that routes for itself
+  g.glu_scale = r.before && !self_route ? r.cw : nullptr;
   u = g;
-  u.codes = up_codes; u.scales = up_scales; u.biases = up_biases;
+  u.codes = r.uc; u.scales = r.usc; u.biases = r.ub;
   const int64_t mt = direct ? n_pairs : max_tiles_for(n_pairs, E, 1, c.tile_rows);
   if (self_route)
-    s = jqk::gemv_gather_route_launch(g, u, plan_gu, rlogits, E, k, renorm, (uint32_t*)idx,
-                                      (float*)cw, T, bits_gu, group_size, x_dtype, sb_dtype,
-                                      y_dtype, st);
+    s = jqk::gemv_gather_route_launch(g, u, plan_gu, r.logits, E, k, r.ro, r.before,
+                                      (uint32_t*)r.idx, (float*)r.cw, T, r.bits_gu, r.gs, r.xd,
+                                      r.sb, r.yd, st);
   else
-    s = grouped_launch(c, g, &u, plan_gu, mt, bits_gu, group_size, x_dtype, sb_dtype, y_dtype, st);
+    s = grouped_launch(c, g, &u, plan_gu, mt, r.bits_gu, r.gs, r.xd, r.sb, r.yd, st);
   if (s) return s;
-  d.x = h_buf; d.codes = down_codes; d.scales = down_scales; d.biases = down_biases; d.y = out;
+  d.x = r.h_buf; d.codes = r.dc; d.scales = r.dsc; d.biases = r.db; d.y = r.y_buf;
   d.M = 1; d.N = H; d.K = I;
-  d.expert_stride_codes = H * (I * bits_d / 32);
-  d.expert_stride_sb = H * (I / group_size);
-  if (comb_out && direct &&
-      jqk::gemv_gather_comb_ok(T, k, H, I, bits_d, group_size, y_dtype, sb_dtype))
-    return jqk::gemv_gather_comb_launch(d, plan, cw, cshared, comb_out, T, k, bits_d,
-                                        group_size, y_dtype, sb_dtype, y_dtype, st);
-  s = grouped_launch(c, d, nullptr, plan, mt, bits_d, group_size, y_dtype, sb_dtype, y_dtype, st);
-  if (s || !comb_out) return s;
-  return jq_moe_combine(out, cw, cshared, T, k, H, comb_out, y_dtype, (jq_stream_t)st);
+  d.expert_stride_codes = H * (I * r.bits_d / 32);
+  d.expert_stride_sb = H * (I / r.gs);
+  if (comb_fused)
+    return jqk::gemv_gather_comb_launch(d, plan, r.comb, T, k, r.bits_d, r.gs, r.yd, r.sb,
+                                        r.yd, st);
+  s = grouped_launch(c, d, nullptr, plan, mt, r.bits_d, r.gs, r.yd, r.sb, r.yd, st);
+  if (s || !r.comb.out) return s;
+  jqk::MoeCombine cc = r.comb;
+  cc.w = r.cw;
+  return combine_launch(r.y_buf, cc, T, k, H, r.yd, st);
 }
+
+MoeRun moe_args(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E,
+                       const uint32_t* idx, int k, const uint32_t* gate_codes,
+                       const void* gate_scales, const void* gate_biases, const uint32_t* up_codes,
+                       const void* up_scales, const void* up_biases, int bits_gu,
+                       const uint32_t* down_codes, const void* down_scales,
+                       const void* down_biases, int bits_d, int sb_dtype, int group_size,
+                       void* h_buf, void* y_buf, int y_dtype, void* workspace,
+                       int64_t workspace_bytes) {
+  MoeRun r;
+  r.x = x; r.xd = x_dtype; r.yd = y_dtype; r.sb = sb_dtype; r.gs = group_size;
+  r.bits_gu = bits_gu; r.bits_d = bits_d; r.k = k;
+  r.T = T; r.H = H; r.I = I; r.E = E;
+  r.idx = idx; r.cw = nullptr; r.logits = nullptr; r.ro = jqr::softmax_opts(1);
+  r.gc = gate_codes; r.gsc = gate_scales; r.gb = gate_biases;
+  r.uc = up_codes; r.usc = up_scales; r.ub = up_biases;
+  r.dc = down_codes; r.dsc = down_scales; r.db = down_biases;
+  r.limit = 0.f; r.before = 0;
+  r.h_buf = h_buf; r.y_buf = y_buf;
+  r.comb.w = nullptr; r.comb.shared = nullptr; r.comb.shared_gate = nullptr;
+  r.comb.out = nullptr; r.comb.before = 0;
+  r.workspace = workspace; r.workspace_bytes = workspace_bytes;
+  return r;
+}
+
+// Workspace of jq_moe_block: the gather plan, then the routed h and slot outputs, then the
+// shared expert's h, up scratch and output.
+struct BlockWs {
+  int64_t plan, h, y, sh_h, sh_up, sh_out, total;
+};
+
+BlockWs block_ws(int64_t T, int64_t H, int64_t I, int64_t E, int k, int64_t shared_I,
+                        int esize) {
+  BlockWs L;
+  int64_t o = 0;
+  L.plan = o; o = align256(o + ws_layout(T * k, E, 1).total);
+  L.h = o; o = align256(o + T * k * I * esize);
+  L.y = o; o = align256(o + T * k * H * esize);
+  L.sh_h = o; o = align256(o + T * shared_I * esize);
+  L.sh_up = o; o = align256(o + T * shared_I * esize);
+  L.sh_out = o; o = align256(o + (shared_I > 0 ? T * H * esize : 0));
+  L.total = o;
+  return L;
+}
+
+bool qweight_ok(const jq_qweight* w) {
+  return w && w->codes && w->scales && w->biases;
+}
+
+}  // namespace
+
+extern "C" {
 
 int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E,
                   const uint32_t* idx, int k, const uint32_t* gate_codes, const void* gate_scales,
@@ -563,11 +726,11 @@ int jq_switch_glu(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, i
                   const void* down_scales, const void* down_biases, int bits_d, int sb_dtype,
                   int group_size, void* h_buf, void* out, int y_dtype, void* workspace,
                   int64_t workspace_bytes, jq_stream_t stream) {
-  return switch_glu_run(x, x_dtype, T, H, I, E, idx, k, gate_codes, gate_scales, gate_biases,
-                        up_codes, up_scales, up_biases, bits_gu, down_codes, down_scales,
-                        down_biases, bits_d, sb_dtype, group_size, h_buf, out, y_dtype,
-                        workspace, workspace_bytes, nullptr, nullptr, nullptr,
-                        (hipStream_t)stream);
+  MoeRun r = moe_args(x, x_dtype, T, H, I, E, idx, k, gate_codes, gate_scales, gate_biases,
+                      up_codes, up_scales, up_biases, bits_gu, down_codes, down_scales,
+                      down_biases, bits_d, sb_dtype, group_size, h_buf, out, y_dtype,
+                      workspace, workspace_bytes);
+  return moe_run(r, (hipStream_t)stream);
 }
 
 int jq_moe_experts(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E,
@@ -580,11 +743,16 @@ int jq_moe_experts(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, 
                    void* workspace, int64_t workspace_bytes, jq_stream_t stream) {
   if (T > 0 && (!logits || !idx || !weights || !out)) return JQ_ERR_NULL;
   if (E <= 0 || E > kMaxExperts || k <= 0 || k > E || k > 64) return JQ_ERR_SHAPE;
-  return switch_glu_run(x, x_dtype, T, H, I, E, idx, k, gate_codes, gate_scales, gate_biases,
-                        up_codes, up_scales, up_biases, bits_gu, down_codes, down_scales,
-                        down_biases, bits_d, sb_dtype, group_size, h_buf, y_buf, y_dtype,
-                        workspace, workspace_bytes, weights, shared, out, (hipStream_t)stream,
-                        logits, renorm);
+  MoeRun r = moe_args(x, x_dtype, T, H, I, E, idx, k, gate_codes, gate_scales, gate_biases,
+                      up_codes, up_scales, up_biases, bits_gu, down_codes, down_scales,
+                      down_biases, bits_d, sb_dtype, group_size, h_buf, y_buf, y_dtype,
+                      workspace, workspace_bytes);
+  r.logits = logits;
+  r.ro = jqr::softmax_opts(renorm);
+  r.cw = weights;
+  r.comb.shared = shared;
+  r.comb.out = out;
+  return moe_run(r, (hipStream_t)stream);
 }
 
 int jq_switch_glu_combine(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
@@ -597,10 +765,93 @@ int jq_switch_glu_combine(const void* x, int x_dtype, int64_t T, int64_t H, int6
                           void* h_buf, void* y_buf, const void* shared, void* out, int y_dtype,
                           void* workspace, int64_t workspace_bytes, jq_stream_t stream) {
   if (T > 0 && (!weights || !out)) return JQ_ERR_NULL;
-  return switch_glu_run(x, x_dtype, T, H, I, E, idx, k, gate_codes, gate_scales, gate_biases,
-                        up_codes, up_scales, up_biases, bits_gu, down_codes, down_scales,
-                        down_biases, bits_d, sb_dtype, group_size, h_buf, y_buf, y_dtype,
-                        workspace, workspace_bytes, weights, shared, out, (hipStream_t)stream);
+  MoeRun r = moe_args(x, x_dtype, T, H, I, E, idx, k, gate_codes, gate_scales, gate_biases,
+                      up_codes, up_scales, up_biases, bits_gu, down_codes, down_scales,
+                      down_biases, bits_d, sb_dtype, group_size, h_buf, y_buf, y_dtype,
+                      workspace, workspace_bytes);
+  r.cw = weights;
+  r.comb.shared = shared;
+  r.comb.out = out;
+  return moe_run(r, (hipStream_t)stream);
+}
+
+int64_t jq_moe_block_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int k,
+                                    int64_t shared_I, int x_dtype) {
+  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0 || shared_I < 0) return -1;
+  if (x_dtype != JQ_BF16 && x_dtype != JQ_F16) return -1;
+  return block_ws(T, H, I, E, k, shared_I, 2).total;
+}
+
+int jq_moe_block(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t E, int k,
+                 const void* logits, int logits_dtype, const jq_route_opts* route,
+                 const jq_qweight* gate,
+                 const jq_qweight* up, const jq_qweight* down, int64_t shared_I,
+                 const jq_qweight* shared_gate_proj, const jq_qweight* shared_up_proj,
+                 const jq_qweight* shared_down_proj, const void* shared_gate_logits,
+                 const jq_moe_opts* opts, uint32_t* idx, float* weights, void* out,
+                 void* workspace, int64_t workspace_bytes, jq_stream_t stream) {
+  if (x_dtype != JQ_BF16 && x_dtype != JQ_F16) return JQ_ERR_DTYPE;
+  if (T < 0 || H <= 0 || I <= 0 || shared_I < 0) return JQ_ERR_SHAPE;
+  if (E <= 0 || E > kMaxExperts || k <= 0 || k > E || k > 64) return JQ_ERR_SHAPE;
+  if (!qweight_ok(gate) || !qweight_ok(up) || !qweight_ok(down)) return JQ_ERR_NULL;
+  if (gate->bits != up->bits || gate->group_size != up->group_size ||
+      down->group_size != gate->group_size)
+    return JQ_ERR_GROUP_SIZE;
+  const int before = opts ? opts->combine : JQ_COMBINE_AFTER_DOWN;
+  const float limit = opts ? opts->swiglu_limit : 0.f;
+  if (before != JQ_COMBINE_AFTER_DOWN && before != JQ_COMBINE_BEFORE_DOWN) return JQ_ERR_SHAPE;
+  if (!(limit >= 0.f) || !isfinite(limit)) return JQ_ERR_SHAPE;
+  if (before && shared_gate_logits) return JQ_ERR_SHAPE;  // the gated shared term is after-down only
+  const bool has_shared = shared_I > 0;
+  if (has_shared && (!qweight_ok(shared_gate_proj) || !qweight_ok(shared_up_proj) ||
+                     !qweight_ok(shared_down_proj)))
+    return JQ_ERR_NULL;
+  if (has_shared && (shared_gate_proj->bits != shared_up_proj->bits ||
+                     shared_gate_proj->group_size != shared_up_proj->group_size))
+    return JQ_ERR_GROUP_SIZE;
+  if (shared_gate_logits && !has_shared) return JQ_ERR_SHAPE;
+  if (!jqh::dtype_ok(logits_dtype)) return JQ_ERR_DTYPE;
+  jqr::RouteOpts ro;
+  int s = route_opts_of(route, E, ro);
+  if (s) return s;
+  ro.logit_dtype = logits_dtype;
+  if (T == 0) return JQ_OK;
+  if (!x || !logits || !idx || !weights || !out) return JQ_ERR_NULL;
+  const BlockWs L = block_ws(T, H, I, E, k, shared_I, 2);
+  if (!workspace || workspace_bytes < L.total) return JQ_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  // The shared expert first: its output joins the combine of the routed experts' launch.
+  void* sh_out = nullptr;
+  if (has_shared) {
+    const jq_qweight* sg = shared_gate_proj;
+    const jq_qweight* su = shared_up_proj;
+    const jq_qweight* sd = shared_down_proj;
+    s = swiglu_run(x, x_dtype, T, shared_I, H, sg->codes, sg->scales, sg->biases, su->codes,
+                   su->scales, su->biases, sg->sb_dtype, sg->bits, sg->group_size,
+                   ws + L.sh_h, ws + L.sh_up, x_dtype, limit, st);
+    if (s) return s;
+    sh_out = ws + L.sh_out;
+    s = jq_quantized_matmul(ws + L.sh_h, x_dtype, sd->codes, sd->scales, sd->biases,
+                            sd->sb_dtype, sd->bits, sd->group_size, T, H, shared_I, sh_out,
+                            x_dtype, stream);
+    if (s) return s;
+  }
+  MoeRun r = moe_args(x, x_dtype, T, H, I, E, idx, k, gate->codes, gate->scales, gate->biases,
+                      up->codes, up->scales, up->biases, gate->bits, down->codes, down->scales,
+                      down->biases, down->bits, gate->sb_dtype, gate->group_size, ws + L.h,
+                      ws + L.y, x_dtype, ws + L.plan, L.h - L.plan);
+  if (up->sb_dtype != r.sb || down->sb_dtype != r.sb) return JQ_ERR_DTYPE;
+  r.logits = logits;
+  r.ro = ro;
+  r.cw = weights;
+  r.limit = limit;
+  r.before = before;
+  r.comb.shared = sh_out;
+  r.comb.shared_gate = shared_gate_logits;
+  r.comb.out = out;
+  r.comb.before = before;
+  return moe_run(r, st);
 }
 
 }  // extern "C"

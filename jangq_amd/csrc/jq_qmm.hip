@@ -322,7 +322,6 @@ JQ_DEV float round_to(float v, int yd) {
 }
 
 // silu(g) * u in fp32 (MLX nn.silu = x * sigmoid(x)).
-JQ_DEV float swiglu(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 // Grouped launch over expert segments. Persistent: block b handles items b, b+grid, ...
 // item = (tile, n-block); tile = (expert, first row, rows) from the device plan.
@@ -388,7 +387,9 @@ __global__ void __launch_bounds__(256) qmm_gather_kernel(QmmProblem p, QmmProble
             const int64_t n = t.n0 + nb + 16 * j + lr;
             if (n < p.N) {
               float v = acc[0][i][j][rr4];
-              if constexpr (C::NB == 2) v = swiglu(round_to(v, yd), round_to(acc[1][i][j][rr4], yd));
+              if constexpr (C::NB == 2)
+                v = jqk::glu_value(round_to(v, yd), round_to(acc[1][i][j][rr4], yd), p.glu_limit,
+                                   p.glu_scale ? p.glu_scale[orow] : 1.f);
               store_out(p.y, orow * p.N + n, v, yd);
             }
           }

@@ -2,7 +2,41 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
+
+#include "jq_common.h"
+
+namespace jqr {
+
+enum { kSoftmax = 0, kSigmoid = 1, kSqrtSoftplus = 2 };
+
+// Device copy of the routing options (jq_route_opts of the C ABI): scores, selection bias,
+// group-limited selection, renormalisation and scaling (jq_route.h).
+struct RouteOpts {
+  int score;          // kSoftmax / kSigmoid / kSqrtSoftplus
+  int renorm;         // divide the k weights by (their sum + eps)
+  float eps;
+  float scale;        // routed scaling factor, applied last
+  const float* bias;  // [E] selection bias or NULL
+  int n_group, topk_group;
+  int logit_dtype;    // JQ_F32 / JQ_BF16 / JQ_F16 logits
+};
+
+inline __host__ __device__ RouteOpts softmax_opts(int renorm) {
+  RouteOpts o;
+  o.score = kSoftmax;
+  o.renorm = renorm;
+  o.eps = 0.f;
+  o.scale = 1.f;
+  o.bias = nullptr;
+  o.n_group = 1;
+  o.topk_group = 1;
+  o.logit_dtype = 0;
+  return o;
+}
+
+}  // namespace jqr
 
 namespace jqk {
 
@@ -31,7 +65,7 @@ int qmv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, i
 // SwiGLU pair at one activation row (b.p[0] gate, b.p[1] up, same x and N): whole rows per
 // wave, h = silu(round(g)) * round(u) written to b.p[0].y (bf16/f16).
 bool gemv_swiglu_ok(int M, int64_t K, int64_t N, int bits, int gs, int xd, int sb, int yd);
-int gemv_swiglu_launch(const QmvBatch& b, int bits, int gs, int xd, int sb, int yd,
+int gemv_swiglu_launch(const QmvBatch& b, int bits, int gs, int xd, int sb, int yd, float limit,
                        hipStream_t st);
 bool gemv_ok(int M, int64_t K, int64_t maxN, int bits, int gs, int xd, int sb);
 int gemv_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
@@ -73,7 +107,25 @@ struct QmmProblem {
   int64_t M, N, K;
   int64_t expert_stride_codes;  // words between experts (gather mode)
   int64_t expert_stride_sb;     // elements between experts' scale rows (gather mode)
+  // SwiGLU pair (gate problem of a gate|up launch): with glu_limit > 0 the rounded gate is
+  // clamped to <= L and the rounded up to [-L, L]; with glu_scale, h = silu(g) * u is
+  // multiplied by glu_scale[output row] before its rounding (routing weights applied before
+  // the down projection).
+  float glu_limit = 0.f;
+  const float* glu_scale = nullptr;
 };
+
+// h = silu(g) * u of a SwiGLU pair whose g and u are already rounded to the output dtype:
+// the optional clamp (jang-tools/jang_tools/dsv41/model.py:1214-1218: up = clip(up, -L, L),
+// gate = min(gate, L)) and the optional per-row factor (the routing weight, model.py:1219-1222).
+JQ_DEV float glu_value(float g, float u, float limit, float factor) {
+  if (limit > 0.f) {
+    g = fminf(g, limit);
+    u = fminf(fmaxf(u, -limit), limit);
+  }
+  const float h = g / (1.0f + expf(-g)) * u;
+  return factor == 1.f ? h : h * factor;
+}
 
 // Decode batches on matrix cores with LDS-streamed weights (jq_dmx.hip): M <= 2*16/(128/gs),
 // gs 64/128, scales of the activation dtype, K % 256 == 0 and K <= 4096 (or K = 1024..2048
@@ -134,22 +186,55 @@ bool gemv_gather_ok(int64_t N, int64_t K, int bits, int gs, int xd, int sb);
 int gemv_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPlan& plan,
                        int64_t max_tiles, int tile_rows, int bits, int gs, int xd, int sb,
                        int yd, hipStream_t st);
+// The MoE combine of a token's k slot outputs y_j (each rounded to the output dtype), the
+// shared expert's output and its optional sigmoid gate:
+//   after the down projection (before = 0): r = round(sum_j w_j * y_j)   (fp32, slot order)
+//     shared term  s' = round(round(sigmoid(gate)) * s)  with a gate, else s;  out = r + s'
+//   before it (before = 1, the weights were applied to h):  out = (sum_j y_j) + s
+// out is rounded by its store. Follows jang-tools/jang_tools/qwen4_exp/modeling.py:594-599
+// and jang-tools/jang_tools/dsv41/model.py:1219-1245 (and the down dispatch of
+// dsv41/metal_decode.py:395-420).
+struct MoeCombine {
+  const float* w;           // [T, k] routing weights (after-down form)
+  const void* shared;       // [T, N] shared expert output, or NULL
+  const void* shared_gate;  // [T] logits of the shared term's gate, or NULL
+  void* out;                // [T, N]
+  int before;
+};
+
+JQ_DEV float round_to_dtype(float v, int yd) {
+  if (yd == 1) return __uint_as_float((uint32_t)jq::f32_to_bf16_bits(v) << 16);
+  if (yd == 2) return jq::f16_bits_to_f32(jq::f32_to_f16_bits(v));
+  return v;
+}
+
+// acc: fp32 slot-order sum (weighted in the after-down form).
+JQ_DEV float moe_final(int before, float acc, bool has_shared, float sh, bool has_gate, float gl,
+                       int yd) {
+  if (before) return has_shared ? acc + sh : acc;
+  const float r = round_to_dtype(acc, yd);
+  if (!has_shared) return r;
+  if (has_gate) sh = round_to_dtype(round_to_dtype(1.0f / (1.0f + expf(-gl)), yd) * sh, yd);
+  return r + sh;
+}
+
 // The same GEMV over a direct plan of T * k pairs (pair t*k + j reads x row t*k + j) with the
-// MoE combine fused in: out[t, n] = round(sum_j w[t*k+j] * round(y[t*k+j, n])) (+ shared[t, n]),
-// slot order in fp32; an expert id outside [0, E) contributes 0. One wave per slot (k <= 16),
-// each over whole rows: K of at most 32 lane chunks or of a single wave.
+// MoE combine fused in (MoeCombine, slot order in fp32); an expert id outside [0, E)
+// contributes 0. One wave per slot (k <= 16), each over whole rows: K of at most 32 lane
+// chunks or of a single wave.
 bool gemv_gather_comb_ok(int64_t T, int k, int64_t N, int64_t K, int bits, int gs, int xd,
                          int sb);
-int gemv_gather_comb_launch(const QmmProblem& p, const GatherPlan& plan, const float* w,
-                            const void* shared, void* out, int64_t T, int k, int bits, int gs,
-                            int xd, int sb, int yd, hipStream_t st);
+int gemv_gather_comb_launch(const QmmProblem& p, const GatherPlan& plan, const MoeCombine& c,
+                            int64_t T, int k, int bits, int gs, int xd, int sb, int yd,
+                            hipStream_t st);
 // The gate|up launch over a direct plan of T * k pairs (x row = pair / k) that routes for
-// itself: pair t*k + j takes the j-th expert of top-k(softmax(logits[t])) (E <= 512), and the
-// token's ids and weights are written to idx / w [T, k] as jq_moe_route writes them.
+// itself: pair t*k + j takes the j-th expert of the token's top-k (jqr::route_wave, E <= 512),
+// and the token's ids and weights are written to idx / w [T, k] as jq_moe_route_ex writes
+// them; with before, h of each pair is multiplied by its weight.
 bool gemv_gather_route_ok(int64_t E, int k);
 int gemv_gather_route_launch(const QmmProblem& g, const QmmProblem& u, const GatherPlan& plan,
-                             const float* logits, int64_t E, int k, int renorm, uint32_t* idx,
-                             float* w, int64_t T, int bits, int gs, int xd, int sb, int yd,
-                             hipStream_t st);
+                             const void* logits, int64_t E, int k, const jqr::RouteOpts& ro,
+                             int before, uint32_t* idx, float* w, int64_t T, int bits, int gs,
+                             int xd, int sb, int yd, hipStream_t st);
 
 }  // namespace jqk

@@ -1,14 +1,27 @@
 // Router top-k of one token in one wave, shared by the route kernel and the expert launch
 // that routes for itself (jq_moe.hip, jq_gemv_gather.hip).
 //
-// softmax(logits) in fp32 (max-subtracted) and the top k by probability, ties to the lower
-// expert id, optionally renormalised to sum 1: the caller-side routing of
-// jang-tools/jang_tools/qwen4_exp/modeling.py:587-593.
+// Scores from the router logits, then the k experts of largest selection value (ties to the
+// lower expert id), in descending order, with their weights:
+//   softmax       p = softmax(logits) in fp32, max-subtracted ("precise")
+//                   jang-tools/jang_tools/qwen4_exp/modeling.py:587-593,
+//                   jang-tools/jang_tools/mistral4_mlx.py:359-387
+//   sigmoid       s = sigmoid(logits)
+//                   jang-tools/jang_tools/dots3/ops.py:149-162, laguna/model.py:50-62
+//   sqrt-softplus s = sqrt(softplus(logits))
+//                   jang-tools/jang_tools/dsv41/model.py:1184-1190
+// The selection value is the score plus an optional per-expert bias (e_score_correction_bias;
+// the weights keep the unbiased score). Group-limited selection (n_group > 1) keeps the
+// topk_group groups of E / n_group consecutive experts with the largest maximum selection
+// value and gives every other expert the selection value 0 and the score 0
+// (mistral4_mlx.py:363-375). The weights are the scores of the chosen experts, optionally
+// divided by (their sum + eps), then multiplied by the routed scaling factor.
 #pragma once
 #include <math.h>
 
 #include "jq_common.h"
 #include "jq_gemv.h"
+#include "jq_qmv.h"
 
 namespace jqr {
 
@@ -60,32 +73,100 @@ JQ_DEV float wave_max_f32(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-// Lane l holds the order keys of logits l, l + 64, ... (SL = ceil(E/64) of them). Top-k in
-// k rounds on the logits (softmax is monotone): each lane offers its largest remaining key
-// and the wave maximum of (key, ~id) picks the round's expert (ties -> lowest id), whose key
-// is then cleared. Lane j < k returns round j's expert and its probability (renormalised over
-// the k when renorm). Every lane of the wave must take part.
+JQ_DEV float lane_read(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// Score of a logit for the sigmoid-type routers (softmax scores need the row's max and sum).
+JQ_DEV float gate_score(int score, float v) {
+  if (score == kSigmoid) return 1.0f / (1.0f + expf(-v));
+  // softplus(v) = max(v, 0) + log1p(exp(-|v|)), then its square root
+  return sqrtf(fmaxf(v, 0.f) + log1pf(expf(-fabsf(v))));
+}
+
+// Lane l holds logits l, l + 64, ... (SL = ceil(E/64) of them). Top-k in k rounds: each lane
+// offers its largest remaining selection key and the wave maximum of (key, ~id) picks the
+// round's expert (ties -> lowest id), whose key is then cleared. Lane j < k returns round j's
+// expert and its weight. Every lane of the wave must take part.
+// row: the token's E logits of o.logit_dtype (converted exactly to fp32).
 template <int SL>
-JQ_DEV void route_wave(const float* __restrict__ row, int E, int k, int renorm, int lane,
+JQ_DEV void route_wave(const void* __restrict__ row, int E, int k, const RouteOpts& o, int lane,
                        uint32_t& id, float& w) {
-  uint32_t key[SL];
+  float v[SL];
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < SL; ++i) {
     const int e = lane + 64 * i;
-    const float v = e < E ? row[e] + 0.0f : -INFINITY;  // + 0: -0 becomes +0
-    key[i] = e < E ? ord_key(v) : 0u;
-    mx = fmaxf(mx, v);
+    float x = -INFINITY;
+    if (e < E) {
+      x = o.logit_dtype == JQ_BF16 ? jq::load_t<JQ_BF16>(row, e)
+          : o.logit_dtype == JQ_F16 ? jq::load_t<JQ_F16>(row, e)
+                                    : ((const float*)row)[e];
+      x += 0.0f;  // -0 becomes +0
+    }
+    v[i] = x;
+    mx = fmaxf(mx, v[i]);
   }
-  mx = wave_max_f32(mx);
-  float sum = 0.f;
+  const bool soft = o.score == kSoftmax;
+  float inv = 1.f;
+  if (soft) {
+    mx = wave_max_f32(mx);
+    float sum = 0.f;
 #pragma unroll
-  for (int i = 0; i < SL; ++i) sum += key[i] ? expf(ord_val(key[i]) - mx) : 0.f;
-  sum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                      __builtin_bit_cast(int, jqg::wave_total_lane63(sum)), 63));
-  const float inv = 1.0f / sum;
+    for (int i = 0; i < SL; ++i) sum += lane + 64 * i < E ? expf(v[i] - mx) : 0.f;
+    sum = lane_read(jqg::wave_total_lane63(sum), 63);
+    inv = 1.0f / sum;
+  }
+  auto score_of = [&](float x) { return soft ? expf(x - mx) * inv : gate_score(o.score, x); };
+  const bool grouped = o.n_group > 1 && o.topk_group < o.n_group;
+  // Selection on the logits themselves when they order the experts as the scores do
+  // (softmax is monotone); otherwise on score + bias.
+  const bool by_logit = soft && !o.bias && !grouped;
+  uint32_t key[SL];
+#pragma unroll
+  for (int i = 0; i < SL; ++i) {
+    const int e = lane + 64 * i;
+    float sel = v[i];
+    if (!by_logit) sel = score_of(v[i]) + (o.bias && e < E ? o.bias[e] : 0.f) + 0.0f;
+    key[i] = e < E ? ord_key(sel) : 0u;
+  }
+  if (grouped) {
+    // Group maxima (lane g holds group g's), the topk_group largest groups kept (ties -> the
+    // lower group), every expert of another group set to selection value 0 and score 0.
+    const int gsz = E / o.n_group;
+    uint32_t gkey = 0;
+    for (int g = 0; g < o.n_group; ++g) {
+      uint32_t m = 0;
+#pragma unroll
+      for (int i = 0; i < SL; ++i) {
+        const int e = lane + 64 * i;
+        m = (e < E && e / gsz == g && key[i] > m) ? key[i] : m;
+      }
+      const uint64_t best = wave_max_u64((uint64_t)m << 32);
+      gkey = lane == g ? (uint32_t)(best >> 32) : gkey;
+    }
+    bool kept = false;
+    for (int r = 0; r < o.topk_group; ++r) {
+      const uint64_t offer = lane < o.n_group && !kept
+                                 ? ((uint64_t)gkey << 32) | (uint32_t)~(uint32_t)lane : 0ull;
+      const uint32_t gid = ~(uint32_t)wave_max_u64(offer);
+      kept = kept || (uint32_t)lane == gid;
+    }
+    const int kept_i = kept ? 1 : 0;
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+      const int e = lane + 64 * i;
+      const int g = e < E ? e / gsz : 0;
+      const int kg = __shfl(kept_i, g, 64);
+      if (e < E && !kg) {
+        key[i] = ord_key(0.0f);
+        v[i] = -INFINITY;  // score 0
+      }
+    }
+  }
 
   uint64_t mine = 0;  // lane j: round j's (key, ~id)
+  float sc = 0.f;     // lane j: round j's score
   for (int j = 0; j < k; ++j) {
     // The lane's largest remaining key; a strict > in slot order keeps the lowest id.
     uint32_t bk = 0;
@@ -99,16 +180,23 @@ JQ_DEV void route_wave(const float* __restrict__ row, int E, int k, int renorm, 
     const uint64_t offer = bk ? ((uint64_t)bk << 32) | (uint32_t)~(uint32_t)(lane + 64 * bi) : 0ull;
     const uint64_t best = wave_max_u64(offer);
     const uint32_t bid = ~(uint32_t)best;
+    float vb = -INFINITY;  // the chosen expert's logit, from its lane
 #pragma unroll
-    for (int i = 0; i < SL; ++i) key[i] = (uint32_t)(lane + 64 * i) == bid ? 0u : key[i];
+    for (int i = 0; i < SL; ++i) {
+      const bool hit = (uint32_t)(lane + 64 * i) == bid;
+      vb = hit ? v[i] : vb;
+      key[i] = hit ? 0u : key[i];
+    }
+    vb = lane_read(vb, (int)(bid & 63u));
     mine = lane == j ? best : mine;
+    sc = lane == j ? vb : sc;
   }
-  const float p = expf(ord_val((uint32_t)(mine >> 32)) - mx) * inv;
-  float wsum = 0.f;  // the k probabilities in round order
-  for (int j = 0; j < k; ++j)
-    wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), j));
+  const float p = lane < k ? score_of(sc) : 0.f;
+  float wsum = 0.f;  // the k scores in round order
+  for (int j = 0; j < k; ++j) wsum += lane_read(p, j);
   id = ~(uint32_t)mine;
-  w = renorm ? p / wsum : p;
+  float r = o.renorm ? p / (wsum + o.eps) : p;
+  w = o.scale == 1.f ? r : r * o.scale;
 }
 
 }  // namespace jqr

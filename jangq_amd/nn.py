@@ -111,12 +111,14 @@ class SwitchGLU(torch.nn.Module):
 
 
 class SharedExpertMLP(torch.nn.Module):
-    """Dense SwiGLU MLP of quantized linears (the shared expert)."""
+    """Dense SwiGLU MLP of quantized linears (the shared expert); swiglu_limit > 0 clamps
+    gate <= L and up to [-L, L] (dsv41/model.py:1237-1245)."""
 
     def __init__(self, dims: int, hidden: int, group_size: int = 64, bits: int = 8, *,
-                 dtype=torch.bfloat16, device=None):
+                 swiglu_limit: float = 0.0, dtype=torch.bfloat16, device=None):
         super().__init__()
         kw = dict(group_size=group_size, bits=bits, dtype=dtype, device=device)
+        self.swiglu_limit = swiglu_limit
         self.gate_proj = QuantizedLinear(dims, hidden, **kw)
         self.up_proj = QuantizedLinear(dims, hidden, **kw)
         self.down_proj = QuantizedLinear(hidden, dims, **kw)
@@ -124,44 +126,83 @@ class SharedExpertMLP(torch.nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         g, u = self.gate_proj, self.up_proj
         h = ops.quantized_swiglu(x, (g.weight, g.scales, g.biases, g.bits),
-                                 (u.weight, u.scales, u.biases, u.bits), g.group_size)
+                                 (u.weight, u.scales, u.biases, u.bits), g.group_size,
+                                 swiglu_limit=self.swiglu_limit)
         return self.down_proj(h)
+
+    def as_tuples(self):
+        """(w, scales, biases, group_size, bits) of gate, up and down (ops.moe_block)."""
+        return tuple((m.weight, m.scales, m.biases, m.group_size, m.bits)
+                     for m in (self.gate_proj, self.up_proj, self.down_proj))
 
 
 class SparseMoeBlock(torch.nn.Module):
-    """Router (quantized gate) -> softmax top-k -> SwitchGLU -> weighted sum (+ shared)."""
+    """Router (quantized gate) -> top-k -> SwitchGLU -> combine with the shared expert.
+
+    Router forms (ops.moe_route): ``score_func`` "softmax" (qwen4_exp/modeling.py:586-593,
+    mistral4_mlx.py:355-387), "sigmoid" (dots3/ops.py:149-162, laguna/model.py:50-62) or
+    "sqrtsoftplus" (dsv41/model.py:1184-1190); ``e_score_bias`` adds a per-expert selection bias
+    (buffer ``e_score_correction_bias``); ``n_group``/``topk_group`` limit the selection to the
+    best groups; ``routed_scaling_factor`` scales the weights.
+    ``shared_expert_gate``: the 1-row linear whose sigmoid scales the shared expert's output
+    (qwen4_exp/modeling.py:583,599). ``combine`` "after" applies the routing weights to the
+    experts' outputs (qwen4 / mlx_lm), "before" to h before the down projection (dsv41);
+    ``swiglu_limit`` is the SwiGLU clamp of dsv41/model.py:1214-1218."""
 
     def __init__(self, dims: int, expert_hidden: int, num_experts: int, top_k: int, *,
                  norm_topk_prob: bool = True, shared_hidden: int | None = None,
                  group_size: int = 64, bits: int = 2, router_bits: int = 8,
-                 shared_bits: int = 8, shared_group_size: int = 64, dtype=torch.bfloat16,
-                 device=None):
+                 shared_bits: int = 8, shared_group_size: int = 64, score_func: str = "softmax",
+                 routed_scaling_factor: float = 1.0, renorm_eps: float | None = None,
+                 e_score_bias: bool = False, n_group: int = 1, topk_group: int = 1,
+                 shared_expert_gate: bool = False, swiglu_limit: float = 0.0,
+                 combine: str = "after", dtype=torch.bfloat16, device=None):
         super().__init__()
+        if shared_expert_gate and not shared_hidden:
+            raise ValueError("shared_expert_gate needs a shared expert")
         self.top_k, self.norm_topk_prob = top_k, norm_topk_prob
+        self.score_func, self.routed_scaling_factor = score_func, routed_scaling_factor
+        self.renorm_eps, self.n_group, self.topk_group = renorm_eps, n_group, topk_group
+        self.swiglu_limit, self.combine = swiglu_limit, combine
         self.gate = QuantizedLinear(dims, num_experts, group_size=64, bits=router_bits,
                                     dtype=dtype, device=device)
         self.switch_mlp = SwitchGLU(dims, expert_hidden, num_experts, group_size=group_size,
                                     bits=bits, dtype=dtype, device=device)
         self.shared_expert = (SharedExpertMLP(dims, shared_hidden, shared_group_size, shared_bits,
-                                              dtype=dtype, device=device)
+                                              swiglu_limit=swiglu_limit, dtype=dtype,
+                                              device=device)
                               if shared_hidden else None)
+        self.shared_expert_gate = (QuantizedLinear(dims, 1, group_size=64, bits=router_bits,
+                                                   dtype=dtype, device=device)
+                                   if shared_expert_gate else None)
+        if e_score_bias:
+            self.register_buffer("e_score_correction_bias",
+                                 torch.zeros(num_experts, dtype=torch.float32, device=device))
+        else:
+            self.e_score_correction_bias = None
+
+    def _route_kw(self):
+        return dict(score=self.score_func, renorm=self.norm_topk_prob, renorm_eps=self.renorm_eps,
+                    scaling=self.routed_scaling_factor, score_bias=self.e_score_correction_bias,
+                    n_group=self.n_group, topk_group=self.topk_group)
 
     def route(self, x: torch.Tensor):
-        logits = self.gate(x).float()
-        return ops.moe_route(logits, self.top_k, self.norm_topk_prob)
+        """(expert ids, weights) of the router for x."""
+        kw = self._route_kw()
+        return ops.moe_route(self.gate(x), self.top_k, kw.pop("renorm"), **kw)
 
     def forward(self, x: torch.Tensor, logits: torch.Tensor | None = None) -> torch.Tensor:
-        # One stream: the shared expert first, so that its output is ready for the launch that
-        # combines the routed experts. (A second stream for it measured no faster inside a HIP
-        # graph, whose replay ran the two branches one after the other, and much slower eagerly.)
-        shared = self.shared_expert(x) if self.shared_expert is not None else None
         if logits is None:
-            logits = self.gate(x).float()
-        # top-k routing, switch_mlp, then (y * scores[..., None]).sum(-2) (+ shared),
-        # qwen4_exp/modeling.py:587-597, as one call: at decode sizes the gate|up launch routes
-        # for itself and the combine runs inside the down-projection launch.
+            logits = self.gate(x)  # the router's bf16/f16 output is read as it is
+        sgl = self.shared_expert_gate(x) if self.shared_expert_gate is not None else None
         m = self.switch_mlp
-        out, _, _ = ops.moe_experts(x, logits, self.top_k, m.gate_proj.as_tuple(),
-                                    m.up_proj.as_tuple(), m.down_proj.as_tuple(),
-                                    m.group_size(), shared, self.norm_topk_prob)
+        # routing, the routed experts, the shared expert and the combine in one call; at decode
+        # sizes the routed experts take two launches (gate|up routing for itself, then down
+        # with the combine inside).
+        out, _, _ = ops.moe_block(
+            x, logits, self.top_k, m.gate_proj.as_tuple(), m.up_proj.as_tuple(),
+            m.down_proj.as_tuple(), m.group_size(),
+            shared=self.shared_expert.as_tuples() if self.shared_expert is not None else None,
+            shared_gate=sgl, combine=self.combine, swiglu_limit=self.swiglu_limit,
+            **self._route_kw())
         return out

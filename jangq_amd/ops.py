@@ -57,6 +57,32 @@ def _codes(w: torch.Tensor) -> torch.Tensor:
     return _dev(w, "packed weight")
 
 
+def _out(out: torch.Tensor | None, shape, like: torch.Tensor, what: str = "out") -> torch.Tensor:
+    """The caller's output tensor, checked (shape, contiguity, device, 16-byte alignment:
+    the kernels write it with vector stores), or a new one of x's dtype."""
+    shape = tuple(int(d) for d in shape)
+    if out is None:
+        return torch.empty(shape, dtype=like.dtype, device=like.device)
+    if tuple(out.shape) != shape:
+        raise ValueError(f"{what} must have shape {shape}, got {tuple(out.shape)}")
+    if out.dtype not in _DT:
+        raise ValueError(f"{what}: unsupported dtype {out.dtype}")
+    if out.device != like.device:
+        raise ValueError(f"{what} must be on {like.device}, got {out.device}")
+    if not out.is_contiguous() or out.data_ptr() % 16:
+        raise ValueError(f"{what} must be contiguous and 16-byte aligned")
+    return out
+
+
+def _sidecars(scales: torch.Tensor, biases: torch.Tensor):
+    """Scales and biases as GPU operands of one dtype (the kernels read both as scales.dtype)."""
+    if biases is None:
+        raise ValueError("affine mode needs biases")
+    if scales.dtype != biases.dtype:
+        raise ValueError(f"scales ({scales.dtype}) and biases ({biases.dtype}) must share a dtype")
+    return _dev(scales, "scales"), _dev(biases, "biases")
+
+
 MX_MODES = {"mxfp4": 4, "mxfp8": 8}
 
 
@@ -104,16 +130,13 @@ def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
         return _mx_dequantize(w, scales, group_size, bits, mode, dtype or torch.bfloat16)
     _check_bits_gs(bits, group_size)
     w = _codes(w)
-    scales = _dev(scales, "scales")
-    biases = _dev(biases, "biases")
+    scales, biases = _sidecars(scales, biases)
     K = packed_in_features(w, bits)
     if scales.shape != biases.shape or scales.shape[:-1] != w.shape[:-1]:
         raise ValueError(f"shape mismatch: w {tuple(w.shape)}, scales {tuple(scales.shape)}, "
                          f"biases {tuple(biases.shape)}")
     if scales.shape[-1] * group_size != K:
         raise ValueError(f"scales width {scales.shape[-1]} x group_size {group_size} != K {K}")
-    if scales.dtype != biases.dtype:
-        raise ValueError("scales and biases must share a dtype")
     out_dtype = dtype or scales.dtype
     rows = math.prod(w.shape[:-1])
     out = torch.empty((*w.shape[:-1], K), dtype=out_dtype, device=w.device)
@@ -175,8 +198,7 @@ def _mx_matmul(x, w, scales, group_size, bits, mode, out):
     if w.dim() != 2 or x.shape[-1] != K:
         raise ValueError(f"x last dim {x.shape[-1]} / w {tuple(w.shape)} do not match K {K}")
     N, M = w.shape[0], math.prod(x.shape[:-1])
-    if out is None:
-        out = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
+    out = _out(out, (*x.shape[:-1], N), x)
     _lib.check(_lib.lib().jq_mx_quantized_matmul(
         _ptr(x), _dtype_code(x, "x"), _ptr(w), _ptr(scales), bits, M, N, K, _ptr(out),
         _dtype_code(out, "output"), _stream()), "quantized_matmul")
@@ -192,12 +214,9 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     if mode in MX_MODES:
         return _mx_matmul(x, w, scales, group_size, bits, mode, out)
     _check_bits_gs(bits, group_size)
-    if biases is None:
-        raise ValueError("affine mode needs biases")
     x = _dev(x, "x")
     w = _codes(w)
-    scales = _dev(scales, "scales")
-    biases = _dev(biases, "biases")
+    scales, biases = _sidecars(scales, biases)
     if w.dim() != 2:
         raise ValueError(f"quantized_matmul expects a 2-D packed weight, got {tuple(w.shape)}")
     N = w.shape[0]
@@ -208,8 +227,7 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
         raise ValueError(f"scales/biases must be {(N, K // group_size)}, got "
                          f"{tuple(scales.shape)} / {tuple(biases.shape)}")
     M = math.prod(x.shape[:-1])
-    if out is None:
-        out = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
+    out = _out(out, (*x.shape[:-1], N), x)
     lib = _lib.lib()
     xd, sd = _dtype_code(x, "x"), _dtype_code(scales, "scales")
     # Decode batches of long rows split K over the kernel's items (fp32 partials in a
@@ -236,15 +254,21 @@ def quantized_matmul_multi(x: torch.Tensor, weights, *, outs=None):
     K = x.shape[-1]
     M = math.prod(x.shape[:-1])
     keep, ys, ws, ss, bs, bits_l, gs_l, ns = [], [], [], [], [], [], [], []
+    if outs is not None and len(outs) != n:
+        raise ValueError(f"outs holds {len(outs)} tensors for {n} weights")
     for i, (w, s, b, gs, bits) in enumerate(weights):
         _check_bits_gs(bits, gs)
-        w, s, b = _codes(w), _dev(s, "scales"), _dev(b, "biases")
-        if packed_in_features(w, bits) != K:
+        w = _codes(w)
+        s, b = _sidecars(s, b)
+        if w.dim() != 2 or packed_in_features(w, bits) != K:
             raise ValueError(f"weight {i}: K mismatch")
+        if tuple(s.shape) != (w.shape[0], K // gs) or s.shape != b.shape:
+            raise ValueError(f"weight {i}: scales/biases must be {(w.shape[0], K // gs)}")
         if s.dtype != weights[0][1].dtype:
             raise ValueError("all scales must share a dtype")
-        y = outs[i] if outs is not None else torch.empty(
-            (*x.shape[:-1], w.shape[0]), dtype=x.dtype, device=x.device)
+        y = _out(None if outs is None else outs[i], (*x.shape[:-1], w.shape[0]), x, f"outs[{i}]")
+        if y.dtype != x.dtype:
+            raise ValueError(f"outs[{i}] must have x's dtype {x.dtype}")
         keep += [w, s, b]
         ys.append(y)
         ws.append(w.data_ptr()); ss.append(s.data_ptr()); bs.append(b.data_ptr())
@@ -258,6 +282,26 @@ def quantized_matmul_multi(x: torch.Tensor, weights, *, outs=None):
         ptrs([y.data_ptr() for y in ys]), _dtype_code(x, "output"), _stream())
     _lib.check(st, "quantized_matmul_multi")
     return ys
+
+
+def _expert_projs(gate, up, down, group_size):
+    """The (codes, scales, biases, bits) of a SwitchGLU's three stacked projections, checked:
+    gate and up share a bit width, and every scale and bias tensor shares one dtype."""
+    out = []
+    for what, (w, s, b, bits) in (("gate", gate), ("up", up), ("down", down)):
+        _check_bits_gs(bits, group_size)
+        s, b = _sidecars(s, b)
+        w = _codes(w)
+        if (w.dim() != 3 or s.dim() != 3 or s.shape != b.shape or s.shape[:2] != w.shape[:2]
+                or s.shape[2] * group_size != packed_in_features(w, bits)):
+            raise ValueError(f"{what}: stacked weights [E, N, K*bits/32] need scales/biases "
+                             f"[E, N, K/{group_size}]")
+        out.append((w, s, b, bits))
+    if out[1][3] != out[0][3]:
+        raise ValueError("gate and up projections must share a bit width")
+    if len({o[1].dtype for o in out}) != 1:
+        raise ValueError("the three projections' scales must share a dtype")
+    return out
 
 
 def _gather_workspace(n_pairs: int, E: int, M: int, device) -> torch.Tensor:
@@ -281,12 +325,9 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     if mode in MX_MODES:
         raise ValueError(f"gather_qmm: mode={mode!r} is not implemented (affine only)")
     _check_bits_gs(bits, group_size)
-    if biases is None:
-        raise ValueError("affine mode needs biases")
     x = _dev(x, "x")
     w = _codes(w)
-    scales = _dev(scales, "scales")
-    biases = _dev(biases, "biases")
+    scales, biases = _sidecars(scales, biases)
     if w.dim() != 3:
         raise ValueError(f"gather_qmm expects stacked weights [E, N, P], got {tuple(w.shape)}")
     if x.dim() < 2:
@@ -322,18 +363,50 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     return out
 
 
-def moe_route(logits: torch.Tensor, k: int, renorm: bool = True):
-    """softmax(logits) in fp32 -> top-k ids (descending) and their probabilities,
-    optionally renormalised to sum 1 (qwen4_exp/modeling.py:587-593)."""
+def _route_opts(score: str, renorm: bool, renorm_eps: float | None, scaling: float,
+                score_bias: torch.Tensor | None, n_group: int, topk_group: int, E: int, device):
+    """(jq_route_opts, tensors to keep alive) after the host-side checks."""
+    if score not in _lib.JQ_SCORE:
+        raise ValueError(f"score={score!r}: expected one of {tuple(_lib.JQ_SCORE)}")
+    keep = []
+    bias_ptr = None
+    if score_bias is not None:
+        b = _dev(score_bias, "score_bias").float().contiguous()
+        if b.numel() != E:
+            raise ValueError(f"score_bias must hold {E} values, got {b.numel()}")
+        keep.append(b)
+        bias_ptr = b.data_ptr()
+    if n_group > 1 and (E % n_group or not 1 <= topk_group <= n_group or n_group > 64):
+        raise ValueError(f"n_group={n_group}, topk_group={topk_group} do not fit {E} experts")
+    eps = (0.0 if score == "softmax" else 1e-20) if renorm_eps is None else float(renorm_eps)
+    o = _lib.RouteOpts(_lib.JQ_SCORE[score], int(bool(renorm)), eps, float(scaling), bias_ptr,
+                       max(int(n_group), 1), int(topk_group))
+    return o, keep
+
+
+def moe_route(logits: torch.Tensor, k: int, renorm: bool = True, *, score: str = "softmax",
+              score_bias: torch.Tensor | None = None, n_group: int = 1, topk_group: int = 1,
+              renorm_eps: float | None = None, scaling: float = 1.0):
+    """Router top-k: scores from the logits (softmax, sigmoid or sqrt-softplus), the k experts
+    of largest score (+ score_bias, for the selection only; optionally group-limited) in
+    descending order, and their unbiased scores, optionally divided by (sum + renorm_eps) and
+    times ``scaling`` (qwen4_exp/modeling.py:587-593, mistral4_mlx.py:355-387,
+    dots3/ops.py:149-162, laguna/model.py:50-62, dsv41/model.py:1184-1190). renorm_eps
+    defaults to 0 for softmax and 1e-20 for the sigmoid-type routers. Logits may be the
+    router's bf16/f16 output (read exactly) or f32."""
     logits = _dev(logits, "logits")
-    if logits.dtype != torch.float32:
-        logits = logits.float()
     E = logits.shape[-1]
     T = math.prod(logits.shape[:-1])
+    if not 1 <= k <= min(E, 64):
+        raise ValueError(f"k={k} must lie in [1, min(E, 64)]")
+    o, keep = _route_opts(score, renorm, renorm_eps, scaling, score_bias, n_group, topk_group, E,
+                          logits.device)
     idx = torch.empty((*logits.shape[:-1], k), dtype=torch.int32, device=logits.device)
     wts = torch.empty((*logits.shape[:-1], k), dtype=torch.float32, device=logits.device)
-    _lib.check(_lib.lib().jq_moe_route(_ptr(logits), T, E, k, int(renorm), _ptr(idx), _ptr(wts),
-                                       _stream()), "moe_route")
+    _lib.check(_lib.lib().jq_moe_route_ex(_ptr(logits), _dtype_code(logits, "logits"), T, E, k,
+                                          _ctypes.byref(o), _ptr(idx), _ptr(wts), _stream()),
+               "moe_route")
+    del keep
     return idx, wts
 
 
@@ -345,14 +418,8 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, down, group_siz
     launch computes gate+up+SiLU for every active expert, a second the down projection."""
     x = _dev(x, "x")
     indices = _dev(indices, "indices")
-    gw, gsc, gb, bits_gu = gate
-    uw, usc, ub, bits_u = up
-    dw, dsc, db, bits_d = down
-    if bits_u != bits_gu:
-        raise ValueError("gate and up projections must share a bit width")
-    _check_bits_gs(bits_gu, group_size)
-    _check_bits_gs(bits_d, group_size)
-    gw, uw, dw = _codes(gw), _codes(uw), _codes(dw)
+    (gw, gsc, gb, bits_gu), (uw, usc, ub, bits_u), (dw, dsc, db, bits_d) = _expert_projs(
+        gate, up, down, group_size)
     E, I = gw.shape[0], gw.shape[1]
     H = x.shape[-1]
     k = indices.shape[-1]
@@ -368,9 +435,9 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, down, group_siz
     sdt = _dtype_code(gsc, "scales")
     _lib.check(_lib.lib().jq_switch_glu(
         _ptr(x), _dtype_code(x, "x"), T, H, I, E, _ptr(idx), k,
-        _ptr(gw), _ptr(_dev(gsc, "scales")), _ptr(_dev(gb, "biases")),
-        _ptr(uw), _ptr(_dev(usc, "scales")), _ptr(_dev(ub, "biases")), bits_gu,
-        _ptr(dw), _ptr(_dev(dsc, "scales")), _ptr(_dev(db, "biases")), bits_d, sdt, group_size,
+        _ptr(gw), _ptr(gsc), _ptr(gb),
+        _ptr(uw), _ptr(usc), _ptr(ub), bits_gu,
+        _ptr(dw), _ptr(dsc), _ptr(db), bits_d, sdt, group_size,
         _ptr(h), _ptr(out), _dtype_code(out, "output"), _ptr(ws), ws.numel(), _stream()),
         "switch_glu")
     return out
@@ -385,14 +452,8 @@ def switch_glu_combine(x: torch.Tensor, indices: torch.Tensor, weights: torch.Te
     sizes the combine runs inside the down-projection launch."""
     x = _dev(x, "x")
     indices = _dev(indices, "indices")
-    gw, gsc, gb, bits_gu = gate
-    uw, usc, ub, bits_u = up
-    dw, dsc, db, bits_d = down
-    if bits_u != bits_gu:
-        raise ValueError("gate and up projections must share a bit width")
-    _check_bits_gs(bits_gu, group_size)
-    _check_bits_gs(bits_d, group_size)
-    gw, uw, dw = _codes(gw), _codes(uw), _codes(dw)
+    (gw, gsc, gb, bits_gu), (uw, usc, ub, bits_u), (dw, dsc, db, bits_d) = _expert_projs(
+        gate, up, down, group_size)
     E, I = gw.shape[0], gw.shape[1]
     H = x.shape[-1]
     k = indices.shape[-1]
@@ -418,9 +479,9 @@ def switch_glu_combine(x: torch.Tensor, indices: torch.Tensor, weights: torch.Te
     sdt = _dtype_code(gsc, "scales")
     _lib.check(_lib.lib().jq_switch_glu_combine(
         _ptr(x), _dtype_code(x, "x"), T, H, I, E, _ptr(idx), _ptr(w), k,
-        _ptr(gw), _ptr(_dev(gsc, "scales")), _ptr(_dev(gb, "biases")),
-        _ptr(uw), _ptr(_dev(usc, "scales")), _ptr(_dev(ub, "biases")), bits_gu,
-        _ptr(dw), _ptr(_dev(dsc, "scales")), _ptr(_dev(db, "biases")), bits_d, sdt, group_size,
+        _ptr(gw), _ptr(gsc), _ptr(gb),
+        _ptr(uw), _ptr(usc), _ptr(ub), bits_gu,
+        _ptr(dw), _ptr(dsc), _ptr(db), bits_d, sdt, group_size,
         _ptr(h), _ptr(ybuf), _ptr(shared), _ptr(out), _dtype_code(out, "output"), _ptr(ws),
         ws.numel(), _stream()), "switch_glu_combine")
     return out
@@ -436,14 +497,8 @@ def moe_experts(x: torch.Tensor, logits: torch.Tensor, k: int, gate, up, down,
     logits = _dev(logits, "logits")
     if logits.dtype != torch.float32:
         logits = logits.float().contiguous()
-    gw, gsc, gb, bits_gu = gate
-    uw, usc, ub, bits_u = up
-    dw, dsc, db, bits_d = down
-    if bits_u != bits_gu:
-        raise ValueError("gate and up projections must share a bit width")
-    _check_bits_gs(bits_gu, group_size)
-    _check_bits_gs(bits_d, group_size)
-    gw, uw, dw = _codes(gw), _codes(uw), _codes(dw)
+    (gw, gsc, gb, bits_gu), (uw, usc, ub, bits_u), (dw, dsc, db, bits_d) = _expert_projs(
+        gate, up, down, group_size)
     E, I = gw.shape[0], gw.shape[1]
     H = x.shape[-1]
     if packed_in_features(gw, bits_gu) != H or dw.shape[1] != H or packed_in_features(dw, bits_d) != I:
@@ -463,11 +518,106 @@ def moe_experts(x: torch.Tensor, logits: torch.Tensor, k: int, gate, up, down,
     ws = _gather_workspace(T * k, E, 1, x.device)
     _lib.check(_lib.lib().jq_moe_experts(
         _ptr(x), _dtype_code(x, "x"), T, H, I, E, _ptr(logits), k, int(renorm), _ptr(idx),
-        _ptr(w), _ptr(gw), _ptr(_dev(gsc, "scales")), _ptr(_dev(gb, "biases")),
-        _ptr(uw), _ptr(_dev(usc, "scales")), _ptr(_dev(ub, "biases")), bits_gu,
-        _ptr(dw), _ptr(_dev(dsc, "scales")), _ptr(_dev(db, "biases")), bits_d,
+        _ptr(w), _ptr(gw), _ptr(gsc), _ptr(gb),
+        _ptr(uw), _ptr(usc), _ptr(ub), bits_gu,
+        _ptr(dw), _ptr(dsc), _ptr(db), bits_d,
         _dtype_code(gsc, "scales"), group_size, _ptr(h), _ptr(ybuf), _ptr(shared), _ptr(out),
         _dtype_code(out, "output"), _ptr(ws), ws.numel(), _stream()), "moe_experts")
+    return out, idx, w
+
+
+def _qweight(w, s, b, bits, group_size, what, keep):
+    """jq_qweight of a checked (codes, scales, biases) triple."""
+    _check_bits_gs(bits, group_size)
+    w = _codes(w)
+    s, b = _sidecars(s, b)
+    if s.shape != b.shape or s.shape[:-1] != w.shape[:-1] or \
+            s.shape[-1] * group_size != packed_in_features(w, bits):
+        raise ValueError(f"{what}: scales/biases must be [..., rows, K/{group_size}]")
+    keep += [w, s, b]
+    return _lib.QWeight(w.data_ptr(), s.data_ptr(), b.data_ptr(), _dtype_code(s, "scales"),
+                        bits, group_size), w
+
+
+def moe_block(x: torch.Tensor, logits: torch.Tensor, k: int, gate, up, down,
+              group_size: int = 64, *, shared=None, shared_gate: torch.Tensor | None = None,
+              score: str = "softmax", renorm: bool = True, renorm_eps: float | None = None,
+              scaling: float = 1.0, score_bias: torch.Tensor | None = None, n_group: int = 1,
+              topk_group: int = 1, combine: str = "after", swiglu_limit: float = 0.0):
+    """A MoE block after its router GEMV, in one call (jq_moe_block): routing (moe_route's
+    options), the routed SwitchGLU (gate/up/down = (w, scales, biases, bits) stacks sharing
+    ``group_size``), the optional shared expert (``shared`` = three (w, scales, biases,
+    group_size, bits) tuples: gate, up, down) with its optional sigmoid gate (``shared_gate``,
+    the [..., 1] output of the 1-row shared_expert_gate linear), and the combine:
+      combine="after"   round(round(sum_j w_j * y_j) + shared term)  (qwen4_exp/modeling.py:594-599)
+      combine="before"  routing weights multiply h before the down projection, then
+                        round(sum_j y_j + shared)                    (dsv41/model.py:1214-1245)
+    swiglu_limit > 0 clamps gate <= L and up to [-L, L] (routed and shared experts).
+    Returns (out [..., H], ids [..., k], weights [..., k])."""
+    x = _dev(x, "x")
+    logits = _dev(logits, "logits")
+    if combine not in _lib.JQ_COMBINE:
+        raise ValueError(f"combine={combine!r}: expected 'after' or 'before'")
+    keep = []
+    qg, gw = _qweight(*gate, group_size, "gate", keep)
+    qu, uw = _qweight(*up, group_size, "up", keep)
+    qd, dw = _qweight(*down, group_size, "down", keep)
+    if gate[3] != up[3]:
+        raise ValueError("gate and up projections must share a bit width")
+    if gw.dim() != 3 or uw.shape != gw.shape or dw.dim() != 3 or dw.shape[0] != gw.shape[0]:
+        raise ValueError("gate/up/down must be expert stacks [E, N, P] of matching E")
+    E, I = gw.shape[0], gw.shape[1]
+    H = x.shape[-1]
+    if packed_in_features(gw, gate[3]) != H or dw.shape[1] != H or \
+            packed_in_features(dw, down[3]) != I:
+        raise ValueError("expert weight shapes do not match x / each other")
+    T = math.prod(x.shape[:-1])
+    if tuple(logits.shape) != (*x.shape[:-1], E):
+        raise ValueError(f"logits must be {(*x.shape[:-1], E)}, got {tuple(logits.shape)}")
+    if not 1 <= k <= min(E, 64):
+        raise ValueError(f"k={k} must lie in [1, min(E, 64)]")
+    ro, rkeep = _route_opts(score, renorm, renorm_eps, scaling, score_bias, n_group, topk_group,
+                            E, x.device)
+    keep += rkeep
+    sI = 0
+    sq = [None, None, None]
+    if shared is not None:
+        (sgw, sgs, sgb, sgg, sgbits), (suw, sus, sub, sug, subits), (sdw, sds, sdb, sdg, sdbits) = shared
+        if sgbits != subits or sgg != sug:
+            raise ValueError("shared gate and up must share bits and group size")
+        sq[0], sgw2 = _qweight(sgw, sgs, sgb, sgbits, sgg, "shared gate", keep)
+        sq[1], suw2 = _qweight(suw, sus, sub, subits, sug, "shared up", keep)
+        sq[2], sdw2 = _qweight(sdw, sds, sdb, sdbits, sdg, "shared down", keep)
+        sI = sgw2.shape[0]
+        if sgw2.dim() != 2 or suw2.shape != sgw2.shape or packed_in_features(sgw2, sgbits) != H \
+                or tuple(sdw2.shape[:1]) != (H,) or packed_in_features(sdw2, sdbits) != sI:
+            raise ValueError("shared expert shapes do not match x")
+    sgl = None
+    if shared_gate is not None:
+        if shared is None:
+            raise ValueError("shared_gate needs a shared expert")
+        if combine != "after":
+            raise ValueError("the gated shared term belongs to combine='after'")
+        sgl = _dev(shared_gate, "shared_gate")
+        if sgl.numel() != T or sgl.dtype != x.dtype:
+            raise ValueError(f"shared_gate must hold {T} values of {x.dtype}")
+    mo = _lib.MoeOpts(_lib.JQ_COMBINE[combine], float(swiglu_limit))
+    lib = _lib.lib()
+    xd = _dtype_code(x, "x")
+    nws = lib.jq_moe_block_workspace_size(T, H, I, E, k, sI, xd)
+    if nws < 0:
+        raise ValueError("moe_block: invalid sizes")
+    ws = torch.empty(max(nws, 256), dtype=torch.uint8, device=x.device)
+    idx = torch.empty((*x.shape[:-1], k), dtype=torch.int32, device=x.device)
+    w = torch.empty((*x.shape[:-1], k), dtype=torch.float32, device=x.device)
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    ref = _ctypes.byref
+    _lib.check(lib.jq_moe_block(
+        _ptr(x), xd, T, H, I, E, k, _ptr(logits), _dtype_code(logits, "logits"), ref(ro),
+        ref(qg), ref(qu), ref(qd), sI, ref(sq[0]) if sq[0] else None,
+        ref(sq[1]) if sq[1] else None, ref(sq[2]) if sq[2] else None, _ptr(sgl), ref(mo),
+        _ptr(idx), _ptr(w), _ptr(out), _ptr(ws), ws.numel(), _stream()), "moe_block")
+    del keep
     return out, idx, w
 
 
@@ -496,9 +646,12 @@ def moe_combine(y: torch.Tensor, weights: torch.Tensor,
     return out
 
 
-def quantized_swiglu(x: torch.Tensor, gate, up, group_size: int = 64) -> torch.Tensor:
+def quantized_swiglu(x: torch.Tensor, gate, up, group_size: int = 64, *,
+                     swiglu_limit: float = 0.0) -> torch.Tensor:
     """silu(gate(x)) * up(x) of a dense MLP, each projection rounded to x.dtype first; gate and
-    up are (w, scales, biases, bits) with the same bits, N and K. One launch at decode sizes."""
+    up are (w, scales, biases, bits) with the same bits, N and K. With swiglu_limit > 0 the
+    rounded gate is clamped to <= L and up to [-L, L] first (dsv41/model.py:1239-1244). One
+    launch at decode sizes."""
     x = _dev(x, "x")
     gw, gsc, gb, bits = gate
     uw, usc, ub, bits_u = up
@@ -506,17 +659,24 @@ def quantized_swiglu(x: torch.Tensor, gate, up, group_size: int = 64) -> torch.T
         raise ValueError("gate and up projections must share a bit width")
     _check_bits_gs(bits, group_size)
     gw, uw = _codes(gw), _codes(uw)
+    gsc, gb = _sidecars(gsc, gb)
+    usc, ub = _sidecars(usc, ub)
+    if usc.dtype != gsc.dtype:
+        raise ValueError("gate and up scales must share a dtype")
     N, K = gw.shape[0], packed_in_features(gw, bits)
     if tuple(uw.shape) != tuple(gw.shape) or x.shape[-1] != K:
         raise ValueError("gate / up / x shapes do not match")
+    if tuple(gsc.shape) != (N, K // group_size) or usc.shape != gsc.shape:
+        raise ValueError(f"gate/up scales and biases must be {(N, K // group_size)}")
     M = math.prod(x.shape[:-1])
     h = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
-    decode = M <= (2 if bits == 2 else 4)
-    up_buf = None if decode else torch.empty_like(h)
-    _lib.check(_lib.lib().jq_quantized_swiglu(
-        _ptr(x), _dtype_code(x, "x"), M, N, K, _ptr(gw), _ptr(_dev(gsc, "scales")),
-        _ptr(_dev(gb, "biases")), _ptr(uw), _ptr(_dev(usc, "scales")), _ptr(_dev(ub, "biases")),
-        _dtype_code(gsc, "scales"), bits, group_size, _ptr(h), _ptr(up_buf),
+    # The up projection's scratch (the library uses it only outside the one-launch decode
+    # forms, whose conditions include the dtypes; always passing it keeps every case valid).
+    up_buf = torch.empty_like(h)
+    _lib.check(_lib.lib().jq_quantized_swiglu_ex(
+        _ptr(x), _dtype_code(x, "x"), M, N, K, _ptr(gw), _ptr(gsc),
+        _ptr(gb), _ptr(uw), _ptr(usc), _ptr(ub),
+        _dtype_code(gsc, "scales"), bits, group_size, float(swiglu_limit), _ptr(h), _ptr(up_buf),
         _dtype_code(h, "output"), _stream()), "quantized_swiglu")
     return h
 

@@ -16,6 +16,14 @@ checkout) in numpy:
   gather_qmm                   naive per-pair loop of jang_tools/dots3/ops_selftest.py:18-28
   switch_glu                   mlx_lm SwitchGLU as restated at dots3/ops.py:195-223
   route_topk                   qwen4_exp/modeling.py:587-593
+  route_scores / route_topk_ex softmax / sigmoid / sqrt-softplus routers with selection bias,
+                               group-limited selection, renorm eps and scaling:
+                               mistral4_mlx.py:355-387, dots3/ops.py:149-162,
+                               laguna/model.py:50-62, dsv41/model.py:1184-1190
+  glu / shared_expert / moe_token  the MoE block's expert MLPs and combine, both forms:
+                               qwen4_exp/modeling.py:586-599 (weights after the down
+                               projection, sigmoid-gated shared term) and dsv41/model.py:
+                               1166-1245 (weights before it, SwiGLU clamp)
   mx_dequantize                OCP MX modes as MLX stores them: mxfp4 per
                                jang-tools/jang_tools/mimo_v2/mxfp4_codec.py:1-50 (E2M1 nibbles,
                                low nibble = even element, E8M0 block scales, 32 per block, the
@@ -34,6 +42,15 @@ How each is pinned (tests/test_oracle.py):
   quantized_matmul  fixture y_ref; brute-force pure-Python loop on tiny shapes
   gather/switch     brute force on tiny shapes; sorted/unsorted equivalence
   route_topk        brute force (full sort) on small shapes
+  route_topk_ex     a pure-Python brute force (explicit sort key, explicit group loop) on
+                    small shapes; closed forms: the sigmoid/sqrt-softplus routers without
+                    bias pick the top-k logits (monotone scores), group-limited selection
+                    with topk_group == n_group is plain top-k, renormalised weights sum to
+                    the scaling factor, softmax matches route_topk
+  moe_token         a per-expert loop restating the reference's array expressions one by
+                    one (tests/test_oracle.py), the "after" form equal to switch_glu +
+                    moe_combine, and the "before" form equal to the "after" form's
+                    per-slot outputs when every weight is 1
 """
 from __future__ import annotations
 
@@ -302,6 +319,101 @@ def route_topk(logits, k: int, renorm: bool = True):
     if renorm:
         w = w / w.sum(axis=-1, keepdims=True)
     return idx.astype(np.int64), w
+
+
+def route_scores(logits, score: str = "softmax") -> np.ndarray:
+    """Router scores in fp64: softmax (qwen4_exp/modeling.py:587, mistral4_mlx.py:359),
+    sigmoid (dots3/ops.py:155, laguna/model.py:52) or sqrt(softplus) (dsv41/model.py:1186)."""
+    z = np.asarray(logits, dtype=np.float64)
+    if score == "softmax":
+        p = np.exp(z - z.max(axis=-1, keepdims=True))
+        return p / p.sum(axis=-1, keepdims=True)
+    if score == "sigmoid":
+        return 1.0 / (1.0 + np.exp(-z))
+    if score == "sqrtsoftplus":
+        return np.sqrt(np.logaddexp(z, 0.0))
+    raise ValueError(score)
+
+
+def route_topk_ex(logits, k: int, *, score: str = "softmax", bias=None, n_group: int = 1,
+                  topk_group: int = 1, renorm: bool = True, eps=None, scaling: float = 1.0):
+    """The routers of the reference in fp64: selection value = score (+ bias), optionally
+    group-limited (the topk_group groups of E/n_group consecutive experts with the largest
+    maximum selection value stay; every other expert gets selection value 0 and score 0,
+    mistral4_mlx.py:363-375), the top k in descending selection order (ties: lower id), their
+    unbiased scores as weights, divided by (sum + eps) with renorm (eps 0 for softmax, 1e-20
+    otherwise: dots3/ops.py:160, laguna/model.py:59) and times ``scaling``
+    (mistral4_mlx.py:385)."""
+    sc = route_scores(logits, score)
+    T, E = sc.shape
+    sel = sc + (0.0 if bias is None else np.asarray(bias, np.float64)[None, :])
+    sc = sc.copy()
+    if n_group > 1 and topk_group < n_group:
+        gsz = E // n_group
+        gmax = sel.reshape(T, n_group, gsz).max(axis=-1)
+        for t in range(T):
+            order = sorted(range(n_group), key=lambda g: (-gmax[t, g], g))
+            for g in order[topk_group:]:
+                sel[t, g * gsz:(g + 1) * gsz] = 0.0
+                sc[t, g * gsz:(g + 1) * gsz] = 0.0
+    idx = np.stack([np.lexsort((np.arange(E), -sel[t]))[:k] for t in range(T)])
+    w = np.take_along_axis(sc, idx, axis=-1)
+    if renorm:
+        e = (0.0 if score == "softmax" else 1e-20) if eps is None else eps
+        w = w / (w.sum(axis=-1, keepdims=True) + e)
+    return idx.astype(np.int64), w * scaling
+
+
+def glu(g, u, limit: float = 0.0, factor=1.0):
+    """silu(g) * u * factor of rounded g, u, with the SwiGLU clamp of
+    jang-tools/jang_tools/dsv41/model.py:1214-1218 (gate = min(gate, L), up = clip(up, -L, L))."""
+    g = np.asarray(g, np.float64)
+    u = np.asarray(u, np.float64)
+    if limit > 0:
+        g = np.minimum(g, limit)
+        u = np.clip(u, -limit, limit)
+    return silu(g) * u * factor
+
+
+def shared_expert(x, Wg, Wu, Wd, limit: float = 0.0, out_dtype: str = "bf16"):
+    """round(down(round(glu(round(x Wg^T), round(x Wu^T))))) of a dense SwiGLU MLP with fp64
+    dequantized weights (qwen4_exp/modeling.py:599; dsv41/model.py:1237-1245)."""
+    x = np.asarray(x, np.float64)
+    g = round_to(x @ Wg.T, out_dtype)
+    u = round_to(x @ Wu.T, out_dtype)
+    h = round_to(glu(g, u, limit), out_dtype).astype(np.float64)
+    return round_to(h @ Wd.T, out_dtype).astype(np.float64)
+
+
+def moe_token(x, ids, w, deq, combine: str = "after", limit: float = 0.0, shared=None,
+              shared_gate=None, out_dtype: str = "bf16"):
+    """One token of a MoE block. deq(which, e) gives expert e's fp64 dequantized 'g', 'u' or 'd'
+    matrix. Per slot: g, u rounded; h = round(glu(g, u, limit, w_j if combine == 'before'));
+    y_j = round(h Wd^T). combine 'after' (qwen4_exp/modeling.py:594-599):
+    round(round(sum_j w_j y_j) + s'), s' = round(round(sigmoid(gate)) * s) with a shared gate;
+    'before' (dsv41/model.py:1219-1245): round(sum_j y_j + s). Returns (out, value before the
+    last rounding)."""
+    x = np.asarray(x, np.float64)
+    acc = np.zeros(deq("d", ids[0]).shape[0], np.float64)
+    for j, e in enumerate(ids):
+        g = round_to(x @ deq("g", e).T, out_dtype)
+        u = round_to(x @ deq("u", e).T, out_dtype)
+        f = w[j] if combine == "before" else 1.0
+        h = round_to(glu(g, u, limit, f), out_dtype).astype(np.float64)
+        y = round_to(h @ deq("d", e).T, out_dtype).astype(np.float64)
+        acc = acc + (y if combine == "before" else w[j] * y)
+    if combine == "before":
+        pre = acc + (0.0 if shared is None else shared)
+        return round_to(pre, out_dtype), pre
+    r = round_to(acc, out_dtype).astype(np.float64)
+    if shared is None:
+        return r, acc
+    sh = np.asarray(shared, np.float64)
+    if shared_gate is not None:
+        gs = round_to(1.0 / (1.0 + np.exp(-float(shared_gate))), out_dtype).astype(np.float64)
+        sh = round_to(gs * sh, out_dtype).astype(np.float64)
+    pre = r + sh
+    return round_to(pre, out_dtype), pre
 
 
 # ----------------------------------------------------------------------------- MX modes

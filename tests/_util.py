@@ -98,3 +98,43 @@ def assert_close(got: np.ndarray, ref: np.ndarray, what: str,
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
     assert r <= rel and m <= mabs, f"{what}: rel_l2={r:.3e} (tol {rel}) max_abs={m:.3e} (tol {mabs})"
     return r, m
+
+
+class RandQ:
+    """A quantized matrix or expert stack built on the GPU from seeded random codes, for the
+    configs' full sizes (a 512-expert stack is too large for the CPU quantizer). Any codes,
+    scales and biases are a valid affine-quantized weight; the scales are positive and the
+    biases centre each group (b ~ -s * (2^bits - 1) / 2), like quantized N(0, std) weights.
+    The oracle reads back only the rows it needs (``host``)."""
+
+    def __init__(self, rows, K, bits, gs, seed, experts=None, std=0.02, sidecar="bf16",
+                 device="cuda"):
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        lead = (rows,) if experts is None else (experts, rows)
+        words = K * bits // 32
+        # int32 words with every bit pattern: two 16-bit halves from randint
+        lo = torch.randint(0, 1 << 16, (*lead, words), generator=g, device=device, dtype=torch.int32)
+        hi = torch.randint(0, 1 << 16, (*lead, words), generator=g, device=device, dtype=torch.int32)
+        self.dw = (hi << 16) | lo
+        qmax = (1 << bits) - 1
+        sdt = {"bf16": torch.bfloat16, "f16": torch.float16}[sidecar]
+        s = (torch.rand((*lead, K // gs), generator=g, device=device) * 1.5 + 0.5) * (
+            4.0 * std / qmax)
+        b = -s * (qmax / 2.0) * (1.0 + 0.1 * torch.randn(s.shape, generator=g, device=device))
+        self.ds, self.db = s.to(sdt), b.to(sdt)
+        self.bits, self.gs, self.sidecar = bits, gs, sidecar
+        self.experts = experts
+
+    def host(self, e=None, rows=None):
+        """(packed uint32, scales f32, biases f32) of expert e (or the 2-D matrix), rows sliced."""
+        sel = (slice(None),) if e is None else (int(e),)
+        if rows is not None:
+            sel = sel + (rows,)
+        w = self.dw[sel].cpu().numpy().view(np.uint32)
+        s = self.ds[sel].float().cpu().numpy()
+        b = self.db[sel].float().cpu().numpy()
+        return w, s, b
+
+    def tup(self):
+        return (self.dw, self.ds, self.db, self.bits)

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol(native_lib):
 
 
 def test_abi_version_and_status_strings(native_lib):
-    assert native_lib.jq_abi_version() == 1
+    assert native_lib.jq_abi_version() == 2
     from jangq_amd import _lib
 
     assert _lib.status_string(0) == "ok"

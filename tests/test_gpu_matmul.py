@@ -170,3 +170,49 @@ def test_multi_matches_single():
         for w, y in zip(ws, ys):
             single = jq.quantized_matmul(tx, w.dw, w.ds, w.db, True, 64, 6)
             assert torch.equal(y, single)
+
+
+def test_operator_argument_checks():
+    """Outputs of the wrong shape, dtype, layout or alignment, and biases whose dtype is not the
+    scales', are rejected before any launch."""
+    qw = QWeight(64, 256, 4, 64, seed=3)
+    x = torch.zeros((2, 256), dtype=torch.bfloat16, device="cuda")
+    for bad in (torch.empty((2, 63), dtype=torch.bfloat16, device="cuda"),
+                torch.empty((64, 2), dtype=torch.bfloat16, device="cuda").t(),
+                torch.empty(2 * 64 + 1, dtype=torch.bfloat16, device="cuda")[1:].view(2, 64),
+                torch.empty((2, 64), dtype=torch.bfloat16)):
+        with pytest.raises(ValueError):
+            jq.quantized_matmul(x, qw.dw, qw.ds, qw.db, True, 64, 4, out=bad)
+    with pytest.raises(ValueError):
+        jq.quantized_matmul(x, qw.dw, qw.ds, qw.db.float(), True, 64, 4)
+    with pytest.raises(ValueError):
+        jq.quantized_matmul_multi(x, [(qw.dw, qw.ds, qw.db, 64, 4)],
+                                  outs=[torch.empty((2, 65), dtype=torch.bfloat16, device="cuda")])
+    with pytest.raises(ValueError):
+        jq.quantized_matmul_multi(x, [(qw.dw, qw.ds, qw.db.half(), 64, 4)])
+    st = QWeight(32, 256, 2, 64, seed=4, experts=4)
+    with pytest.raises(ValueError):
+        jq.gather_qmm(x[:, None, :], st.dw, st.ds, st.db.float(),
+                      rhs_indices=torch.zeros(2, dtype=torch.int32, device="cuda"),
+                      group_size=64, bits=2)
+    d = QWeight(256, 32, 2, 32, seed=5, experts=4)
+    idx = torch.zeros((2, 1), dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError):  # down at group 32 with gate/up at 64
+        jq.switch_glu(x, idx, (st.dw, st.ds, st.db, 2), (st.dw, st.ds, st.db, 2),
+                      (d.dw, d.ds, d.db, 2), 64)
+
+
+@pytest.mark.parametrize("sdt", ["f32", "bf16"])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_quantized_swiglu_decode_dtypes(xdt, sdt):
+    """One activation row with f32 activations or f32 scales (outside the one-launch decode
+    forms) still runs: the up projection's scratch is always passed."""
+    N, K, gs = 96, 512, 64
+    g = QWeight(N, K, 4, gs, seed=11, sidecar=sdt)
+    u = QWeight(N, K, 4, gs, seed=12, sidecar=sdt)
+    rng = np.random.default_rng(13)
+    x = O.round_to(rng.standard_normal((1, K), dtype=np.float32), xdt)
+    h = jq.quantized_swiglu(to_tensor(x, xdt), (g.dw, g.ds, g.db, 4), (u.dw, u.ds, u.db, 4), gs)
+    ref = O.swiglu_pair(x, (g.packed, g.s, g.b, 4), (u.packed, u.s, u.b, 4), gs, xdt)
+    tol = dict(rel=2e-6, mabs=1e-4) if xdt == "f32" else {}
+    assert_close(values_of(h), ref, f"swiglu x {xdt} scales {sdt}", **tol)

@@ -315,3 +315,172 @@ def test_moe_experts(T, k, E, H, I, with_shared, renorm):
     assert torch.equal(ids, ids2) and torch.equal(w, w2)
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
     np.testing.assert_array_equal(ids.cpu().numpy(), O.route_topk(logits, k, renorm)[0])
+
+
+@pytest.mark.parametrize("score", ["softmax", "sigmoid", "sqrtsoftplus"])
+@pytest.mark.parametrize("T,E,k,groups,with_bias,ldt", [
+    (3, 64, 4, (1, 1), False, "f32"),
+    (2, 512, 10, (1, 1), True, "bf16"),   # config-5 width, bf16 router output read directly
+    (4, 256, 8, (8, 4), True, "f32"),     # group-limited, DeepSeek-like
+    (5, 640, 6, (4, 1), False, "f16"),    # more experts than the in-launch routing holds
+])
+def test_route_variants(score, T, E, k, groups, with_bias, ldt):
+    """Every router form against the oracle: ids equal, weights within fp32 rounding."""
+    rng = np.random.default_rng(E + k + T)
+    logits = O.round_to(rng.standard_normal((T, E)).astype(np.float32) * 2, ldt)
+    bias = rng.standard_normal(E).astype(np.float32) * 0.2 if with_bias else None
+    ng, tg = groups
+    tb = torch.from_numpy(bias).cuda() if with_bias else None
+    idx, w = jq.moe_route(to_tensor(logits, ldt), k, True, score=score, score_bias=tb,
+                          n_group=ng, topk_group=tg, scaling=1.5)
+    ridx, rw = O.route_topk_ex(logits, k, score=score, bias=bias, n_group=ng, topk_group=tg,
+                               renorm=True, scaling=1.5)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
+    _, w0 = jq.moe_route(to_tensor(logits, ldt), k, False, score=score, score_bias=tb,
+                         n_group=ng, topk_group=tg)
+    np.testing.assert_allclose(w0.cpu().numpy(), O.route_topk_ex(
+        logits, k, score=score, bias=bias, n_group=ng, topk_group=tg, renorm=False)[1],
+        rtol=1e-5, atol=1e-7)
+
+
+def _moe_case(E, H, I, bits, gs, sI, seed):
+    g = QWeight(I, H, bits, gs, seed=seed, experts=E)
+    u = QWeight(I, H, bits, gs, seed=seed + 1, experts=E)
+    d = QWeight(H, I, bits, gs, seed=seed + 2, experts=E)
+    sh = None
+    if sI:
+        sh = [QWeight(sI, H, 8, 64, seed=seed + 3), QWeight(sI, H, 8, 64, seed=seed + 4),
+              QWeight(H, sI, 8, 64, seed=seed + 5)]
+    return g, u, d, sh
+
+
+@pytest.mark.parametrize("T", [1, 5, 64])
+@pytest.mark.parametrize("combine,limit,gated,score", [
+    ("after", 0.0, False, "softmax"),
+    ("after", 0.5, True, "softmax"),
+    ("before", 0.0, False, "sqrtsoftplus"),
+    ("before", 0.5, False, "sigmoid"),
+])
+def test_moe_block(T, combine, limit, gated, score):
+    """jq_moe_block against the oracle's MoE token (both combine forms, the SwiGLU clamp, the
+    sigmoid-gated shared term, sigmoid / sqrt-softplus routers with a selection bias and a
+    scaling factor): T = 1 takes the two fused decode launches, T = 5 the routing launch and
+    one-row tiles, T = 64 the plan and matrix-core tiles."""
+    E, H, I, k, gs, sI = 32, 512, 256, 4, 64, 256
+    g, u, d, sh = _moe_case(E, H, I, 2, gs, sI, seed=70)
+    rng = np.random.default_rng(T * 11 + len(combine))
+    x = O.round_bf16(rng.standard_normal((T, H), dtype=np.float32))
+    logits = O.round_bf16(rng.standard_normal((T, E)).astype(np.float32))
+    bias = None if score == "softmax" else rng.standard_normal(E).astype(np.float32) * 0.1
+    rsf = 1.0 if score == "softmax" else 2.0
+    gl = O.round_bf16(rng.standard_normal(T).astype(np.float32)) if gated else None
+    tsh = tuple((q.dw, q.ds, q.db, 64, 8) for q in sh)
+    out, ids, w = jq.moe_block(
+        to_tensor(x, "bf16"), to_tensor(logits, "bf16"), k, (g.dw, g.ds, g.db, 2),
+        (u.dw, u.ds, u.db, 2), (d.dw, d.ds, d.db, 2), gs, shared=tsh,
+        shared_gate=None if gl is None else to_tensor(gl, "bf16")[:, None], score=score,
+        score_bias=None if bias is None else torch.from_numpy(bias).cuda(), scaling=rsf,
+        combine=combine, swiglu_limit=limit)
+    ridx, rw = O.route_topk_ex(logits, k, score=score, bias=bias, scaling=rsf)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ridx)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
+    cache = {}
+
+    def deq(c, e):
+        key = (c, int(e))
+        if key not in cache:
+            q = {"g": g, "u": u, "d": d}[c]
+            cache[key] = O.dequantize_affine(q.packed[e], q.s[e], q.b[e], 2, gs).astype(np.float64)
+        return cache[key]
+
+    Ws = [q.dequant().astype(np.float64) for q in sh]
+    yv = values_of(out)
+    for t in sorted({0, T // 2, T - 1}):
+        s_out = O.shared_expert(x[t], *Ws, limit=limit)
+        ref, pre = O.moe_token(x[t], ridx[t], rw[t], deq, combine, limit, s_out,
+                               None if gl is None else gl[t])
+        assert_close(yv[t], ref, f"moe_block T{T} t{t} {combine} L{limit}", exact=pre,
+                     out_dtype="bf16")
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_moe_block_equals_experts_call(T):
+    """The default block (softmax, after-down combine, no clamp) is bit-identical to the shared
+    expert's two calls followed by jq_moe_experts with its output."""
+    E, H, I, k, gs, sI = 64, 512, 256, 6, 128, 512
+    g, u, d, sh = _moe_case(E, H, I, 2, gs, sI, seed=80)
+    rng = np.random.default_rng(T)
+    x = to_tensor(O.round_bf16(rng.standard_normal((T, H), dtype=np.float32)), "bf16")
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).cuda()
+    tsh = tuple((q.dw, q.ds, q.db, 64, 8) for q in sh)
+    out, ids, w = jq.moe_block(x, logits, k, (g.dw, g.ds, g.db, 2), (u.dw, u.ds, u.db, 2),
+                               (d.dw, d.ds, d.db, 2), gs, shared=tsh)
+    hs = jq.quantized_swiglu(x, (sh[0].dw, sh[0].ds, sh[0].db, 8), (sh[1].dw, sh[1].ds, sh[1].db, 8), 64)
+    s_out = jq.quantized_matmul(hs, sh[2].dw, sh[2].ds, sh[2].db, True, 64, 8)
+    out2, ids2, w2 = jq.moe_experts(x, logits, k, (g.dw, g.ds, g.db, 2), (u.dw, u.ds, u.db, 2),
+                                    (d.dw, d.ds, d.db, 2), gs, s_out)
+    assert torch.equal(ids, ids2) and torch.equal(w, w2)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+
+
+def test_moe_block_argument_errors():
+    E, H, I, gs = 8, 256, 128, 64
+    g, u, d, sh = _moe_case(E, H, I, 2, gs, 128, seed=90)
+    x = torch.zeros((1, H), dtype=torch.bfloat16, device="cuda")
+    lg = torch.zeros((1, E), device="cuda")
+    gt, ut, dt_ = (g.dw, g.ds, g.db, 2), (u.dw, u.ds, u.db, 2), (d.dw, d.ds, d.db, 2)
+    tsh = tuple((q.dw, q.ds, q.db, 64, 8) for q in sh)
+    with pytest.raises(ValueError):  # gated shared term without a shared expert
+        jq.moe_block(x, lg, 2, gt, ut, dt_, gs, shared_gate=x[:, :1])
+    with pytest.raises(ValueError):  # gated shared term in the before-down form
+        jq.moe_block(x, lg, 2, gt, ut, dt_, gs, shared=tsh, shared_gate=x[:, :1], combine="before")
+    with pytest.raises(ValueError):  # groups that do not divide E
+        jq.moe_block(x, lg, 2, gt, ut, dt_, gs, n_group=3, topk_group=1)
+    with pytest.raises(ValueError):
+        jq.moe_block(x, lg, 2, gt, ut, dt_, gs, score="relu")
+    with pytest.raises(ValueError):
+        jq.moe_block(x, lg[:, :4], 2, gt, ut, dt_, gs)
+
+
+@pytest.mark.parametrize("T", [1, 6])
+def test_moe_block_module_shared_gate(T):
+    """SparseMoeBlock with the qwen-style shared_expert_gate (a 1-row 8-bit linear whose
+    sigmoid scales the shared expert's output, qwen4_exp/modeling.py:599), bf16 router logits
+    read directly."""
+    H, I, E, k, sI = 256, 128, 16, 4, 256
+    blk = jnn.SparseMoeBlock(H, I, E, k, shared_hidden=sI, bits=2, shared_expert_gate=True,
+                             device="cuda")
+    qs = {}
+
+    def fill(name, lin, rows, K, bits, seed, experts=None):
+        q = QWeight(rows, K, bits, 64, seed=seed, experts=experts)
+        lin.weight, lin.scales, lin.biases = q.dw, q.ds, q.db
+        qs[name] = q
+
+    fill("r", blk.gate, E, H, 8, 20)
+    fill("sg_lin", blk.shared_expert_gate, 1, H, 8, 21)
+    for n, lin, rows, K, seed in (("g", blk.switch_mlp.gate_proj, I, H, 22),
+                                  ("u", blk.switch_mlp.up_proj, I, H, 23),
+                                  ("d", blk.switch_mlp.down_proj, H, I, 24)):
+        fill(n, lin, rows, K, 2, seed, E)
+    for n, lin, rows, K, seed in (("sg", blk.shared_expert.gate_proj, sI, H, 25),
+                                  ("su", blk.shared_expert.up_proj, sI, H, 26),
+                                  ("sd", blk.shared_expert.down_proj, H, sI, 27)):
+        fill(n, lin, rows, K, 8, seed)
+    rng = np.random.default_rng(T)
+    x = O.round_bf16(rng.standard_normal((T, H), dtype=np.float32))
+    y = values_of(blk(to_tensor(x, "bf16")))
+    deqd = {n: q.dequant().astype(np.float64) for n, q in qs.items() if n in ("r", "sg_lin", "sg", "su", "sd")}
+    logits = O.round_bf16(x.astype(np.float64) @ deqd["r"].T)
+    gl = O.round_bf16(x.astype(np.float64) @ deqd["sg_lin"].T)[:, 0]
+    ids, w = O.route_topk(logits, k)
+
+    def deq(c, e):
+        q = qs[c]
+        return O.dequantize_affine(q.packed[e], q.s[e], q.b[e], 2, 64).astype(np.float64)
+
+    for t in range(T):
+        s_out = O.shared_expert(x[t], deqd["sg"], deqd["su"], deqd["sd"])
+        ref, pre = O.moe_token(x[t], ids[t], w[t], deq, "after", 0.0, s_out, gl[t])
+        assert_close(y[t], ref, f"gated block t{t}", exact=pre, out_dtype="bf16")

@@ -15,6 +15,8 @@ import ctypes
 import json
 from pathlib import Path
 
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -464,3 +466,139 @@ def test_mx_layout_and_brute_force():
                     e, m = (byte >> 3) & 15, byte & 7
                     v = sgn * (m * 2.0 ** -9 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7))
                 assert got[r, k] == np.float32(v * 2.0 ** (int(sc[r, k // 32]) - 127)), (mode, r, k)
+
+
+def _route_brute(logits, k, score, bias, n_group, topk_group, renorm, eps, scaling):
+    """Pure-Python restatement of the reference routers, token by token (math module only)."""
+    import math as m
+    out_i, out_w = [], []
+    for row in np.asarray(logits, np.float64).tolist():
+        E = len(row)
+        if score == "softmax":
+            mx = max(row)
+            ex = [m.exp(v - mx) for v in row]
+            tot = sum(ex)
+            sc = [v / tot for v in ex]
+        elif score == "sigmoid":
+            sc = [1.0 / (1.0 + m.exp(-v)) for v in row]
+        else:
+            sc = [m.sqrt(m.log1p(m.exp(-abs(v))) + max(v, 0.0)) for v in row]
+        sel = [sc[e] + (0.0 if bias is None else float(bias[e])) for e in range(E)]
+        if n_group > 1 and topk_group < n_group:
+            gsz = E // n_group
+            best = [max(sel[g * gsz:(g + 1) * gsz]) for g in range(n_group)]
+            kept = sorted(range(n_group), key=lambda g: (-best[g], g))[:topk_group]
+            for e in range(E):
+                if e // gsz not in kept:
+                    sel[e] = 0.0
+                    sc[e] = 0.0
+        ids = sorted(range(E), key=lambda e: (-sel[e], e))[:k]
+        w = [sc[e] for e in ids]
+        if renorm:
+            tot = sum(w) + eps
+            w = [v / tot for v in w]
+        out_i.append(ids)
+        out_w.append([v * scaling for v in w])
+    return np.array(out_i), np.array(out_w)
+
+
+@pytest.mark.parametrize("score", ["softmax", "sigmoid", "sqrtsoftplus"])
+@pytest.mark.parametrize("groups", [(1, 1), (4, 2), (8, 3)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_route_topk_ex_vs_brute_force(score, groups, with_bias):
+    rng = np.random.default_rng(zlib.crc32(repr((score, groups, with_bias)).encode()))
+    T, E, k = 5, 32, 4
+    logits = rng.standard_normal((T, E)).astype(np.float32) * 2
+    bias = rng.standard_normal(E).astype(np.float32) * 0.3 if with_bias else None
+    ng, tg = groups
+    eps = 0.0 if score == "softmax" else 1e-20
+    idx, w = O.route_topk_ex(logits, k, score=score, bias=bias, n_group=ng, topk_group=tg,
+                             renorm=True, scaling=2.5)
+    bi, bw = _route_brute(logits, k, score, bias, ng, tg, True, eps, 2.5)
+    np.testing.assert_array_equal(idx, bi)
+    np.testing.assert_allclose(w, bw, rtol=1e-12)
+    np.testing.assert_allclose(w.sum(-1), 2.5, rtol=1e-12)  # renormalised, then scaled
+    _, w0 = O.route_topk_ex(logits, k, score=score, bias=bias, n_group=ng, topk_group=tg,
+                            renorm=False)
+    np.testing.assert_allclose(w0, _route_brute(logits, k, score, bias, ng, tg, False, 0, 1)[1],
+                               rtol=1e-12)
+
+
+def test_route_topk_ex_closed_forms():
+    rng = np.random.default_rng(51)
+    logits = rng.standard_normal((7, 64)).astype(np.float32) * 3
+    ref_i, ref_w = O.route_topk(logits, 6)
+    i0, w0 = O.route_topk_ex(logits, 6)
+    np.testing.assert_array_equal(i0, ref_i)
+    np.testing.assert_allclose(w0, ref_w, rtol=1e-12)
+    for score in ("sigmoid", "sqrtsoftplus"):  # monotone scores without bias: the top logits
+        i1, _ = O.route_topk_ex(logits, 6, score=score)
+        np.testing.assert_array_equal(i1, ref_i)
+    # keeping every group is no grouping at all
+    i2, w2 = O.route_topk_ex(logits, 6, n_group=8, topk_group=8)
+    np.testing.assert_array_equal(i2, ref_i)
+    # the bias changes the selection but not the weights' source: weights are unbiased scores
+    bias = np.zeros(64, np.float32)
+    bias[:8] = 10.0
+    i3, w3 = O.route_topk_ex(logits, 6, score="sigmoid", bias=bias, renorm=False)
+    assert np.all(i3 < 8)
+    np.testing.assert_allclose(w3, 1 / (1 + np.exp(-np.take_along_axis(
+        logits.astype(np.float64), i3, -1))), rtol=1e-12)
+    # planted mistake: weights taken from the biased values differ from the reference's
+    wrong = np.take_along_axis(1 / (1 + np.exp(-logits.astype(np.float64))) + bias, i3, -1)
+    assert not np.allclose(wrong, w3)
+    # group-limited: only experts of the kept groups are chosen when they hold enough
+    i4, _ = O.route_topk_ex(logits, 4, n_group=8, topk_group=2)
+    for t in range(7):
+        assert len(set((i4[t] // 8).tolist())) <= 2
+
+
+def test_moe_token_forms_vs_compositions():
+    """moe_token against the reference's array expressions evaluated with torch (CPU, fp64,
+    rounded to bf16 where the reference's arrays are bf16): qwen4_exp/modeling.py:594-599
+    ('after', sigmoid-gated shared term) and dsv41/model.py:1214-1245 ('before', clamp)."""
+    import torch
+
+    rng = np.random.default_rng(61)
+    H, I, E, k = 64, 32, 6, 3
+    Ws = {(c, e): rng.standard_normal((I, H) if c != "d" else (H, I)) * 0.1
+          for c in "gud" for e in range(E)}
+    deq = lambda c, e: Ws[(c, int(e))]  # noqa: E731
+    x = O.round_bf16(rng.standard_normal(H).astype(np.float32)).astype(np.float64)
+    ids = np.array([4, 1, 3])
+    w = np.array([0.5, 0.3, 0.2])
+    sh = O.round_bf16(rng.standard_normal(H).astype(np.float32)).astype(np.float64)
+    bf = lambda t: t.to(torch.bfloat16).double()  # noqa: E731
+    tx = torch.from_numpy(x)
+    lim = 0.8
+    for combine in ("after", "before"):
+        for gate in (None, 0.7):
+            if combine == "before" and gate is not None:
+                continue
+            got, _ = O.moe_token(x, ids, w, deq, combine, lim, sh, gate)
+            ys = []
+            for j, e in enumerate(ids):
+                g = bf(tx @ torch.from_numpy(deq("g", e)).T).clamp(max=lim)
+                u = bf(tx @ torch.from_numpy(deq("u", e)).T).clamp(-lim, lim)
+                h = torch.nn.functional.silu(g) * u
+                if combine == "before":
+                    h = h * w[j]
+                ys.append(bf(bf(h) @ torch.from_numpy(deq("d", e)).T))
+            if combine == "after":
+                routed = bf(sum(wj * y for wj, y in zip(w, ys)))
+                term = torch.from_numpy(sh)
+                if gate is not None:
+                    term = bf(bf(torch.sigmoid(torch.tensor(gate, dtype=torch.float64))) * term)
+                ref = bf(routed + term)
+            else:
+                ref = bf(sum(ys) + torch.from_numpy(sh))
+            np.testing.assert_array_equal(got, ref.float().numpy())
+    # the 'after' form without clamp is switch_glu's slots combined by moe_combine
+    got, _ = O.moe_token(x, ids, w, deq, "after", 0.0, sh)
+    slots = []
+    for e in ids:
+        g = O.round_bf16(x @ deq("g", e).T)
+        u = O.round_bf16(x @ deq("u", e).T)
+        h = O.round_bf16(O.silu(g) * u)
+        slots.append(O.round_bf16(h.astype(np.float64) @ deq("d", e).T))
+    np.testing.assert_array_equal(got, O.moe_combine(np.array(slots)[None], w[None], sh[None])[0])
