@@ -10,6 +10,7 @@ from .ops import (  # noqa: F401
     dequantize_tensor,
     expand_packed_1bit_to_2bit,
     gather_qmm,
+    moe_block,
     moe_combine,
     moe_experts,
     moe_route,
@@ -25,7 +26,7 @@ from ._lib import JangqError  # noqa: F401
 from .shapes import bit_inference, infer_bits_group_size  # noqa: F401
 
 __all__ = [
-    "dequantize", "dequantize_tensor", "expand_packed_1bit_to_2bit", "gather_qmm", "moe_combine", "moe_experts", "moe_route", "quantize", "quantized_matmul",
+    "dequantize", "dequantize_tensor", "expand_packed_1bit_to_2bit", "gather_qmm", "moe_block", "moe_combine", "moe_experts", "moe_route", "quantize", "quantized_matmul",
     "quantized_matmul_multi", "quantized_swiglu", "switch_glu", "switch_glu_combine", "unpack", "bit_inference", "infer_bits_group_size",
     "JangqError",
 ]

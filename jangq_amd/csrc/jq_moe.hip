@@ -657,13 +657,12 @@ int moe_run(MoeRun& r, hipStream_t st) {
   d.M = 1; d.N = H; d.K = I;
   d.expert_stride_codes = H * (I * r.bits_d / 32);
   d.expert_stride_sb = H * (I / r.gs);
-  if (comb_fused)
-    return jqk::gemv_gather_comb_launch(d, plan, r.comb, T, k, r.bits_d, r.gs, r.yd, r.sb,
-                                        r.yd, st);
-  s = grouped_launch(c, d, nullptr, plan, mt, r.bits_d, r.gs, r.yd, r.sb, r.yd, st);
-  if (s || !r.comb.out) return s;
   jqk::MoeCombine cc = r.comb;
   cc.w = r.cw;
+  if (comb_fused)
+    return jqk::gemv_gather_comb_launch(d, plan, cc, T, k, r.bits_d, r.gs, r.yd, r.sb, r.yd, st);
+  s = grouped_launch(c, d, nullptr, plan, mt, r.bits_d, r.gs, r.yd, r.sb, r.yd, st);
+  if (s || !r.comb.out) return s;
   return combine_launch(r.y_buf, cc, T, k, H, r.yd, st);
 }
 

@@ -83,17 +83,23 @@ def half_ulp(v: np.ndarray, dtype: str) -> np.ndarray:
 
 
 def assert_close(got: np.ndarray, ref: np.ndarray, what: str,
-                 rel=REL_L2_TOL, mabs=MAX_ABS_TOL, exact=None, out_dtype=None):
+                 rel=REL_L2_TOL, mabs=MAX_ABS_TOL, exact=None, out_dtype=None, ulps=0.5):
     """rel-L2 of got against ref (the reference rounded to the output dtype) and max-abs
     error. With `exact` (the unrounded fp32/fp64 accumulation) the max-abs bound applies to
-    |got - exact| beyond the output rounding itself (half an ulp of out_dtype): an output
-    that rounds the other way at a rounding boundary is then not charged a full ulp."""
+    |got - exact| beyond the output rounding itself (ulps = half an ulp of out_dtype): an
+    output that rounds the other way at a rounding boundary is then not charged a full ulp.
+
+    Composite outputs (a MoE block: gate/up, h and each expert's output are rounded to the
+    activation dtype before the next stage, as the reference's arrays are) pass ulps=1: an
+    intermediate value within fp32-vs-fp64 accumulation noise of a rounding midpoint may round
+    the other way, and that one-ulp step moves every output of the next matmul slightly, so
+    some outputs legitimately land one ulp from the fp64 chain's rounding."""
     r = O.rel_l2(got, ref)
     if exact is None:
         m = O.max_abs(got, ref)
     else:
         dev = np.abs(np.asarray(got, np.float64) - np.asarray(exact, np.float64))
-        m = float(np.max(dev - half_ulp(exact, out_dtype))) if dev.size else 0.0
+        m = float(np.max(dev - 2 * ulps * half_ulp(exact, out_dtype))) if dev.size else 0.0
         m = max(m, 0.0)
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
     assert r <= rel and m <= mabs, f"{what}: rel_l2={r:.3e} (tol {rel}) max_abs={m:.3e} (tol {mabs})"
@@ -119,8 +125,10 @@ class RandQ:
         self.dw = (hi << 16) | lo
         qmax = (1 << bits) - 1
         sdt = {"bf16": torch.bfloat16, "f16": torch.float16}[sidecar]
-        s = (torch.rand((*lead, K // gs), generator=g, device=device) * 1.5 + 0.5) * (
-            4.0 * std / qmax)
+        # uniform codes have std qmax / sqrt(12): scales around std * sqrt(12) / qmax give
+        # weights of standard deviation ~std, as a quantized N(0, std) matrix has
+        s = (torch.rand((*lead, K // gs), generator=g, device=device) * 0.5 + 0.75) * (
+            std * 12 ** 0.5 / qmax)
         b = -s * (qmax / 2.0) * (1.0 + 0.1 * torch.randn(s.shape, generator=g, device=device))
         self.ds, self.db = s.to(sdt), b.to(sdt)
         self.bits, self.gs, self.sidecar = bits, gs, sidecar
@@ -128,9 +136,11 @@ class RandQ:
 
     def host(self, e=None, rows=None):
         """(packed uint32, scales f32, biases f32) of expert e (or the 2-D matrix), rows sliced."""
-        sel = (slice(None),) if e is None else (int(e),)
+        sel = () if e is None else (int(e),)
         if rows is not None:
             sel = sel + (rows,)
+        if not sel:
+            sel = (slice(None),)
         w = self.dw[sel].cpu().numpy().view(np.uint32)
         s = self.ds[sel].float().cpu().numpy()
         b = self.db[sel].float().cpu().numpy()

@@ -4,7 +4,9 @@ The weights are seeded random codes built on the GPU (tests._util.RandQ): a 512-
 stack is too large for the CPU quantizer, and any codes, scales and biases are a valid
 affine weight. The oracle dequantizes only what a checked output needs (the selected
 experts of sampled tokens, a column slice of a prefill output) and accumulates in fp64.
-Tolerances: rel-L2 <= 1e-3 and max-abs <= 2e-2 beyond the output rounding (north star).
+Tolerances: rel-L2 <= 1e-3 and max-abs <= 2e-2 beyond the output rounding (north star); the
+MoE block outputs, whose stages round to bf16 in turn, are allowed one output ulp for that
+rounding (tests._util.assert_close, ulps=1).
 
 Config 5 routing follows its recipe: logits ~N(0,1) with +2 on round(0.1 * 512) = 51
 experts chosen by a seeded permutation, softmax -> top-10 -> renormalise, plus the
@@ -54,11 +56,12 @@ def _moe_token_oracle(x, ids, w, g, u, d, shared=None):
     return O.round_bf16(r), r
 
 
-def _shared_oracle(x, sg, su, sd):
+def _shared_oracle(x, sg, su, sd, pre=False):
     gv = _rb(x @ _deq(sg).T)
     uv = _rb(x @ _deq(su).T)
     h = _rb(O.silu(gv) * uv)
-    return _rb(h @ _deq(sd).T)
+    y = h @ _deq(sd).T
+    return (_rb(y), y) if pre else _rb(y)
 
 
 def _skewed_logits(T, E, seed, skew):
@@ -113,10 +116,10 @@ def _check_block(blk, qs, T, E, H, k, seed, skew, sample):
             sh = _shared_oracle(x[t].astype(np.float64), qs["sg"], qs["su"], qs["sd"])
         ref, pre = _moe_token_oracle(x[t].astype(np.float64), ids[t], w[t], qs["g"], qs["u"],
                                      qs["d"], sh)
-        assert_close(y[t], ref, f"block token {t}", exact=pre, out_dtype="bf16")
+        assert_close(y[t], ref, f"block token {t}", exact=pre, out_dtype="bf16", ulps=1)
         if sh is None:
             assert_close(values_of(out)[t], ref, f"moe_experts token {t}", exact=pre,
-                         out_dtype="bf16")
+                         out_dtype="bf16", ulps=1)
 
 
 @pytest.fixture(scope="module")
@@ -148,8 +151,8 @@ def test_c5_router_and_shared_full_size(c5_block):
         assert_close(lg, O.round_bf16(ref), f"router T{T}", exact=ref, out_dtype="bf16")
         sh = values_of(blk.shared_expert(tx))
         for t in (0, T - 1):
-            r = _shared_oracle(x[t].astype(np.float64), qs["sg"], qs["su"], qs["sd"])
-            assert_close(sh[t], r, f"shared T{T} t{t}")
+            r, pre = _shared_oracle(x[t].astype(np.float64), qs["sg"], qs["su"], qs["sd"], True)
+            assert_close(sh[t], r, f"shared T{T} t{t}", exact=pre, out_dtype="bf16", ulps=1)
 
 
 @pytest.fixture(scope="module")
@@ -245,4 +248,5 @@ def test_routed_gateup_at_h4096(E, k, I, gs):
     rid, rw = O.route_topk(logits, k)
     np.testing.assert_array_equal(ids.cpu().numpy(), rid)
     ref, pre = _moe_token_oracle(x[0].astype(np.float64), rid[0], rw[0], g, u, d)
-    assert_close(values_of(out)[0], ref, f"routed gate|up E{E} k{k}", exact=pre, out_dtype="bf16")
+    assert_close(values_of(out)[0], ref, f"routed gate|up E{E} k{k}", exact=pre, out_dtype="bf16",
+                 ulps=1)
