@@ -128,6 +128,23 @@ int jq_quantized_matmul_ws(const void* x, int x_dtype, const uint32_t* codes,
                            jq_stream_t stream);
 
 /*
+ * jq_quantized_matmul_ws without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid it); it has no
+ * counterpart in the reference. The K-split partials of decode batches of long rows go to a
+ * fixed array inside the library, JQ_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on
+ * a GPU until the process ends; a shape that needs more returns JQ_ERR_WORKSPACE (the size
+ * query jq_quantized_matmul_workspace_size tells it beforehand). Every other shape runs as
+ * jq_quantized_matmul. It calls no allocator. Calls that overlap on one GPU (other streams or
+ * threads) share the array and race; the array keeps the last call's contents, and each call
+ * writes every partial it reads.
+ */
+#define JQ_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int jq_quantized_matmul_noalloc(const void* x, int x_dtype, const uint32_t* codes,
+                                const void* scales, const void* biases, int sb_dtype, int bits,
+                                int group_size, int64_t M, int64_t N, int64_t K, void* y,
+                                int y_dtype, jq_stream_t stream);
+
+/*
  * Grouped form of jq_quantized_matmul: `count` independent problems sharing x_dtype,
  * y_dtype and sb_dtype, in ONE launch when they share M, K, bits and group_size (q/k/v or
  * gate/up projections of one token batch). Each array has `count` entries.

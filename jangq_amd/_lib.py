@@ -61,6 +61,7 @@ SIGNATURES = {
          _P, _P, _P, _P, _P, _P, _I,
          _P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _L, _P],
     ),
+    "jq_quantized_matmul_noalloc": (_I, [_P, _I, _P, _P, _P, _I, _I, _I, _L, _L, _L, _P, _I, _P]),
     "jq_moe_route_ex": (_I, [_P, _I, _L, _L, _I, _P, _P, _P, _P]),
     "jq_quantized_swiglu_ex": (
         _I,
