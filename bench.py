@@ -39,9 +39,12 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true")
     p.add_argument("--only", default="", help="comma list of extra workloads to run")
-    p.add_argument("--profile", choices=("gateup", "copy"), default=None,
-                   help="run only the dominant kernel (gateup) or a plain 256 MiB copy (copy), "
-                        "eagerly, for rocprofv3 counter passes; prints one JSON line")
+    p.add_argument("--profile", choices=("gateup", "copy", "down", "c1", "c3", "c5"),
+                   default=None,
+                   help="run one workload eagerly for rocprofv3 counter passes and print one "
+                        "JSON line: the gate|up launch (gateup), a plain 256 MiB copy (copy), "
+                        "the 2-bit down projection (down), config 1 (c1), or the MoE layer of "
+                        "config 3 / 5 at T = 1 (c3, c5)")
     return p.parse_args()
 
 
@@ -227,6 +230,21 @@ def moe_layer(gen, E, H, I, bits, gs, k, shared_I=None):
     return blk, router
 
 
+def _clone_dense(blk):
+    """A copy of the block whose router and shared expert are new tensors (the expert stacks
+    are shared: the rotated routings already spread them over more than the cache holds)."""
+    import copy
+
+    c = copy.copy(blk)
+    c._modules = dict(blk._modules)
+    for name in ("gate", "shared_expert"):
+        m = blk._modules.get(name)
+        if m is not None:
+            mc = copy.deepcopy(m)
+            c._modules[name] = mc
+    return c
+
+
 def bench_moe(gen, name, E, H, I, bits, gs, k, T, steps, warmup, shared_I=None, skew=False):
     import torch
 
@@ -242,11 +260,18 @@ def bench_moe(gen, name, E, H, I, bits, gs, k, T, steps, warmup, shared_I=None, 
             perm = torch.randperm(E, generator=gen, device="cuda")[: round(0.1 * E)]
             lg[:, perm] += 2.0
         logit_sets.append(lg)
+    # Rotated copies of the router and the shared expert: every step reads a copy the previous
+    # steps evicted (their bytes over the copies exceed twice the last-level cache).
+    dense = router.nbytes() + (3 * (shared_I * H + shared_I * (H // 64) * 4) if shared_I else 0)
+    C = copies_for(dense)
+    blocks = [blk] + [_clone_dense(blk) for _ in range(C - 1)]
+
     def step(i):
         # The router GEMV runs (its bytes are counted below); routing uses the config's
         # synthetic N(0,1) logits so that the expert load is the one the config states.
-        blk.gate(xs[i % R])
-        return blk(xs[i % R], logits=logit_sets[i % R])
+        b = blocks[i % C]
+        b.gate(xs[i % R])
+        return b(xs[i % R], logits=logit_sets[i % R])
 
     ms = timed(step, steps, warmup)
     # Algorithmic bytes of one layer: router + distinct selected experts (+ shared).
@@ -256,11 +281,32 @@ def bench_moe(gen, name, E, H, I, bits, gs, k, T, steps, warmup, shared_I=None, 
         idx, _ = jq.moe_route(lg, k)
         distinct.append(len(torch.unique(idx)))
     mean_distinct = sum(distinct) / len(distinct)
-    nb = router.nbytes() + mean_distinct * per_expert
-    if shared_I:
-        nb += 3 * (shared_I * H + shared_I * (H // 64) * 4)
+    nb = dense + mean_distinct * per_expert
     return dict(ms=ms, tokens_per_s=T / ms * 1e3, distinct_experts=mean_distinct,
-                bytes=nb, gbs=nb / ms / 1e6, frac=nb / ms / 1e6 / HBM_PEAK_GBS)
+                bytes=nb, gbs=nb / ms / 1e6, frac=nb / ms / 1e6 / HBM_PEAK_GBS,
+                dense_copies=C)
+
+
+def bench_attn8(gen, T, steps, warmup):
+    """Config 5's attention projections at 8-bit g64 (geometry of config 2: q/o 4096 x 4096,
+    k/v 1024 x 4096): q|k|v grouped, then o, rotated copies."""
+    import jangq_amd as jq
+
+    H = 4096
+    q, kk, v, o = (QW(randn((n, H), 0.02, gen), 8, 64) for n in (4096, 1024, 1024, 4096))
+    x = randn((T, H), 1.0, gen)
+    wb = sum(w.nbytes() for w in (q, kk, v, o))
+    R = copies_for(wb)
+    sets = [(q, kk, v, o)] + [tuple(w.clone() for w in (q, kk, v, o)) for _ in range(R - 1)]
+
+    def step(i):
+        a, b, c, d = sets[i % R]
+        jq.quantized_matmul_multi(x, [a.tup(), b.tup(), c.tup()])
+        return jq.quantized_matmul(x, d.w, d.s, d.b, True, 64, 8)
+
+    ms = timed(step, steps, warmup)
+    nb = wb + 2 * T * H * 2 + 2 * T * (4096 + 2048 + 4096)
+    return dict(ms=ms, bytes=nb, gbs=nb / ms / 1e6, frac=nb / ms / 1e6 / HBM_PEAK_GBS, copies=R)
 
 
 # ----------------------------------------------------------------------------- CPU baseline
@@ -312,6 +358,87 @@ def cpu_baseline_c2(min_seconds=10.0, max_seconds=30.0):
             "dequant_s": round(t_deq, 3), "matmul_s": round(t_mm, 3)}
 
 
+def _rand_qweight(rng, rows, K, bits, gs):
+    """Random packed codes with bf16-valued scales / biases (any codes are a valid weight)."""
+    import numpy as np
+
+    from oracle import jangq_oracle as O
+
+    words = rng.integers(0, 1 << 32, size=(rows, K * bits // 32), dtype=np.uint64).astype(np.uint32)
+    qmax = (1 << bits) - 1
+    s = O.round_bf16((rng.random((rows, K // gs), dtype=np.float32) * 0.5 + 0.75) * (0.07 / qmax))
+    b = O.round_bf16(-s * (qmax / 2))
+    return words, s, b
+
+
+def cpu_baseline_moe(min_seconds=8.0, max_seconds=20.0):
+    """Config-3 MoE decode on the host, the reference's per-active-expert loop
+    (dots3/ops_selftest.py:18-28): per token, softmax top-4 of 128 logits, then for each
+    selected expert numpy dequant (affine.py:445-463) of gate/up/down and fp32 BLAS matvecs,
+    silu(g) * u, the weighted sum. Tokens until min_seconds of work."""
+    import numpy as np
+
+    from oracle import jangq_oracle as O
+
+    rng = np.random.default_rng(301)
+    E, H, I, k, gs = 128, 4096, 2048, 4, 64
+    pool = 16  # distinct expert weights generated (a token's experts are drawn from them)
+    experts = [[_rand_qweight(rng, r, c, 2, gs) for r, c in ((I, H), (I, H), (H, I))]
+               for _ in range(pool)]
+    t_deq = t_mm = 0.0
+    tokens = 0
+    while t_deq + t_mm < min_seconds and t_deq + t_mm < max_seconds:
+        x = O.round_bf16(rng.standard_normal(H, dtype=np.float32))
+        logits = rng.standard_normal((1, E)).astype(np.float32)
+        idx, w = O.route_topk(logits, k)
+        out = np.zeros(H, np.float32)
+        for j, e in enumerate(idx[0]):
+            mats = experts[int(e) % pool]
+            t0 = time.perf_counter()
+            Wg, Wu, Wd = (O.dequantize_affine(p, sc, bi, 2, gs) for p, sc, bi in mats)
+            t1 = time.perf_counter()
+            g, u = x @ Wg.T, x @ Wu.T
+            out += np.float32(w[0, j]) * ((g / (1 + np.exp(-g)) * u) @ Wd.T)
+            t2 = time.perf_counter()
+            t_deq += t1 - t0
+            t_mm += t2 - t1
+        tokens += 1
+    secs = t_deq + t_mm
+    return {"value": round(tokens / secs, 3), "unit": "tokens/s",
+            "sample": f"{tokens} config-3 tokens at T = 1 (4 experts each, 2-bit g64, H 4096, "
+                      f"I 2048): numpy dequant {t_deq:.2f} s + BLAS matvecs {t_mm:.2f} s",
+            "dequant_s": round(t_deq, 3), "matmul_s": round(t_mm, 3)}
+
+
+def cpu_baseline_prefill(bits=4, min_seconds=5.0):
+    """Config-4 prefill on the host: numpy dequant of the 14336 x 4096 weight then fp32 BLAS
+    x @ W^T with x [2048, 4096]; passes until min_seconds."""
+    import numpy as np
+
+    from oracle import jangq_oracle as O
+
+    rng = np.random.default_rng(401)
+    M, K, N, gs = 2048, 4096, 14336, 64
+    p, sc, bi = _rand_qweight(rng, N, K, bits, gs)
+    x = O.round_bf16(rng.standard_normal((M, K), dtype=np.float32))
+    t_deq = t_mm = 0.0
+    passes = 0
+    while t_deq + t_mm < min_seconds:
+        t0 = time.perf_counter()
+        W = O.dequantize_affine(p, sc, bi, bits, gs)
+        t1 = time.perf_counter()
+        _ = x @ W.T
+        t2 = time.perf_counter()
+        t_deq += t1 - t0
+        t_mm += t2 - t1
+        passes += 1
+    flops = 2.0 * M * N * K * passes
+    return {"value": round(flops / (t_deq + t_mm) / 1e12, 4), "unit": "TFLOP/s",
+            "sample": f"{passes} passes of config 4 ({bits}-bit): numpy dequant {t_deq:.2f} s + "
+                      f"BLAS fp32 GEMM {t_mm:.2f} s",
+            "dequant_s": round(t_deq, 3), "matmul_s": round(t_mm, 3)}
+
+
 # ----------------------------------------------------------------------------- counters
 
 TRAFFIC_FILE = ROOT / "profiles" / "gateup_c2_m1_traffic.txt"
@@ -345,6 +472,34 @@ def profile_run(kind, steps):
         return {"profile": "copy", "bytes_read": n, "bytes_written": n, "launches": steps}
     import jangq_amd as jq
 
+    if kind in ("c3", "c5"):
+        E, I, gs, k, sI = (128, 2048, 64, 4, None) if kind == "c3" else (512, 1024, 128, 10, 4096)
+        blk, _ = moe_layer(gen, E, 4096, I, 2, gs, k, sI)
+        xs = [randn((1, 4096), 1.0, gen) for _ in range(16)]
+        lgs = []
+        for _ in range(16):
+            lg = torch.randn((1, E), generator=gen, device="cuda")
+            if kind == "c5":
+                lg[:, torch.randperm(E, generator=gen, device="cuda")[: round(0.1 * E)]] += 2.0
+            lgs.append(lg)
+        for i in range(steps):
+            blk.gate(xs[i % 16])
+            blk(xs[i % 16], logits=lgs[i % 16])
+        torch.cuda.synchronize()
+        return {"profile": kind, "launches": steps}
+    if kind in ("down", "c1"):
+        N, K, bits = (4096, 14336, 2) if kind == "down" else (4096, 4096, 4)
+        w = QW(randn((N, K), 0.02, gen), bits, 64)
+        R = copies_for(w.nbytes())
+        ws = [w] + [w.clone() for _ in range(R - 1)]
+        x = randn((1, K), 1.0, gen)
+        for i in range(steps):
+            q = ws[i % R]
+            jq.quantized_matmul(x, q.w, q.s, q.b, True, 64, bits)
+        torch.cuda.synchronize()
+        return {"profile": kind, "algorithmic_bytes": w.nbytes() + 2 * K + 2 * N,
+                "launches": steps, "copies": R}
+
     layer, acts, _, _ = c2_block(gen, 1)
     R = copies_for(layer["g"].nbytes() + layer["u"].nbytes())
     gs = [(layer["g"], layer["u"])] + [(layer["g"].clone(), layer["u"].clone())
@@ -367,7 +522,9 @@ def main():
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 "
                                    "(multi-GPU sharding is a design note, not a run)"}))
         sys.exit(2)
-    os.environ.setdefault("OMP_NUM_THREADS", str(len(os.sched_getaffinity(0))))
+    ncores = str(len(os.sched_getaffinity(0)))
+    for var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
+        os.environ.setdefault(var, ncores)
     import torch
 
     from jangq_amd import _lib
@@ -413,10 +570,18 @@ def main():
             r = bench_moe(gen, "c5", 512, 4096, 1024, 2, 128, 10, T, s2, w2, shared_I=4096,
                           skew=True)
             extra[f"c5_moe_T{T}"] = {k: round(v, 4) for k, v in r.items()}
+            r = bench_attn8(gen, T, s2, w2)
+            extra[f"c5_attention_8bit_T{T}"] = {k: round(v, 4) for k, v in r.items()}
 
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline_c2()
+        cpu["other"] = {"c3_moe_T1": cpu_baseline_moe(),
+                        "c4_prefill_4bit": cpu_baseline_prefill(4)}
+        cpu["note"] = ("the oracle's restatement of the reference CPU path (kind port); its 3/6-bit "
+                       "unpack is vectorised where the reference loops per element "
+                       "(pack.py:132-149), so those figures flatter the reference; the MLX CPU "
+                       "backend does not exist off Apple silicon and is not timed")
 
     line = {
         "metric": "decode quant-GEMV HBM GB/s (% of 8 TB/s peak); MoE layer tokens/sec",

@@ -102,8 +102,19 @@ def pack_bits(values, bits: int) -> np.ndarray:
 
 
 def unpack_bits(packed, bits: int, count: int) -> np.ndarray:
-    """Inverse of pack_bits; any array shape is flattened as its row-major byte stream."""
+    """Inverse of pack_bits; any array shape is flattened as its row-major byte stream.
+    1/2/4/8 bits: the reference's shift-and-mask fast paths (pack.py:101-130); 3/5/6 bits: a
+    vectorised bit-plane unpack (the reference loops per element there, pack.py:132-149)."""
     b = np.asarray(packed, dtype=np.uint8).reshape(-1)
+    if bits == 8:
+        return b[:count].copy()
+    if bits in (1, 2, 4):
+        per = 8 // bits
+        mask = (1 << bits) - 1
+        out = np.empty(b.size * per, dtype=np.uint8)
+        for i in range(per):
+            out[i::per] = (b >> (i * bits)) & mask
+        return out[:count]
     stream = np.unpackbits(b, bitorder="little")[: count * bits]
     planes = stream.reshape(count, bits).astype(np.uint16)
     return (planes << np.arange(bits, dtype=np.uint16)[None, :]).sum(axis=1).astype(np.uint8)
