@@ -571,6 +571,12 @@ struct MoeRun {
   jqk::MoeCombine comb;  // comb.out NULL: no combine (jq_switch_glu)
   void* workspace;
   int64_t workspace_bytes;
+  // shared expert inside the routed gate|up launch (jq_moe_block, one token): its
+  // gate/up/down, intermediate size, h buffer and output
+  const jq_qweight *sg, *su, *sd;
+  int64_t sI;
+  void* sh_h;
+  void* sh_out;
 };
 
 int moe_run(MoeRun& r, hipStream_t st) {
@@ -687,7 +693,72 @@ MoeRun moe_args(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int
   r.comb.w = nullptr; r.comb.shared = nullptr; r.comb.shared_gate = nullptr;
   r.comb.out = nullptr; r.comb.before = 0;
   r.workspace = workspace; r.workspace_bytes = workspace_bytes;
+  r.sg = r.su = r.sd = nullptr;
+  r.sI = 0;
+  r.sh_h = nullptr;
+  r.sh_out = nullptr;
   return r;
+}
+
+// Whether one token's MoE block runs the shared expert's gate|up inside the routed gate|up
+// launch (jq_moe_fused.h): bf16 throughout, routing in the gate|up launch, the combine in the
+// down launch, and the instantiated widths (routed 2..4 bits, shared 4 or 8 bits). Measured on
+// MI355X at config 5 (T = 1): one launch of 31.3 us against 24.5 + 10.4 us for the two. The
+// shared down projection and the routed down-with-combine stay two launches: a single launch
+// that joined them (the last wave of each row group finishing it) measured 23.0 us against
+// 11.3 + 7.3 us, the routed half being latency-bound at one 16-wave block per CU.
+bool fused_ok(const MoeRun& r) {
+  if (r.T != 1 || r.sI <= 0 || !r.sg || !r.logits || !r.comb.out) return false;
+  if (r.xd != JQ_BF16 || r.yd != JQ_BF16 || r.sb != JQ_BF16) return false;
+  if (r.sg->sb_dtype != JQ_BF16 || r.su->sb_dtype != JQ_BF16) return false;
+  auto lowbits = [](int b) { return b >= 2 && b <= 4; };
+  if (!lowbits(r.bits_gu) || (r.sg->bits != 4 && r.sg->bits != 8)) return false;
+  if (!jqk::gemv_gather_route_ok(r.E, r.k)) return false;
+  if (!jqk::gemv_gather_ok(r.I, r.H, r.bits_gu, r.gs, r.xd, r.sb) ||
+      jqk::fused_rw(r.H, r.bits_gu) > 2)
+    return false;
+  if (!jqk::gemv_gather_comb_ok(1, r.k, r.H, r.I, r.bits_d, r.gs, r.yd, r.sb)) return false;
+  return jqk::gemv_swiglu_ok(1, r.H, r.sI, r.sg->bits, r.sg->group_size, r.xd, JQ_BF16, r.yd);
+}
+
+int moe_run_fused(MoeRun& r, hipStream_t st) {
+  const int64_t H = r.H, I = r.I, E = r.E;
+  const int k = r.k;
+  jqk::GatherPlan plan = direct_plan(r.idx, k, E, nullptr);
+  jqk::GatherPlan plan_gu = plan;
+  plan_gu.pair_div = k;
+  plan_gu.x_rows = 1;
+  plan.x_rows = k;
+  jqk::QmmProblem g, u, d;
+  g.x = r.x; g.codes = r.gc; g.scales = r.gsc; g.biases = r.gb; g.y = r.h_buf;
+  g.M = 1; g.N = I; g.K = H;
+  g.expert_stride_codes = I * (H * r.bits_gu / 32);
+  g.expert_stride_sb = I * (H / r.gs);
+  g.glu_limit = r.limit;
+  u = g;
+  u.codes = r.uc; u.scales = r.usc; u.biases = r.ub;
+  jqk::QmvProblem sg, su;
+  sg.x = r.x; sg.codes = r.sg->codes; sg.scales = r.sg->scales; sg.biases = r.sg->biases;
+  sg.y = r.sh_h; sg.N = r.sI;
+  su = sg;
+  su.codes = r.su->codes; su.scales = r.su->scales; su.biases = r.su->biases;
+  int s = jqk::moe_fused_gu_launch(g, u, plan_gu, r.logits, E, k, r.ro, r.before,
+                                   (uint32_t*)r.idx, (float*)r.cw, r.bits_gu, r.gs, sg, su,
+                                   r.sg->bits, r.sg->group_size, r.limit, st);
+  if (s) return s;
+  // the shared expert's down projection, then the routed down with the combine
+  s = jq_quantized_matmul(r.sh_h, r.xd, r.sd->codes, r.sd->scales, r.sd->biases,
+                          r.sd->sb_dtype, r.sd->bits, r.sd->group_size, 1, H, r.sI, r.sh_out,
+                          r.xd, (jq_stream_t)st);
+  if (s) return s;
+  d.x = r.h_buf; d.codes = r.dc; d.scales = r.dsc; d.biases = r.db; d.y = r.y_buf;
+  d.M = 1; d.N = H; d.K = I;
+  d.expert_stride_codes = H * (I * r.bits_d / 32);
+  d.expert_stride_sb = H * (I / r.gs);
+  jqk::MoeCombine c = r.comb;
+  c.w = r.cw;
+  c.shared = r.sh_out;
+  return jqk::gemv_gather_comb_launch(d, plan, c, 1, k, r.bits_d, r.gs, r.yd, r.sb, r.yd, st);
 }
 
 // Workspace of jq_moe_block: the gather plan, then the routed h and slot outputs, then the
@@ -820,7 +891,37 @@ int jq_moe_block(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, in
   if (!workspace || workspace_bytes < L.total) return JQ_ERR_WORKSPACE;
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
-  // The shared expert first: its output joins the combine of the routed experts' launch.
+  MoeRun r = moe_args(x, x_dtype, T, H, I, E, idx, k, gate->codes, gate->scales, gate->biases,
+                      up->codes, up->scales, up->biases, gate->bits, down->codes, down->scales,
+                      down->biases, down->bits, gate->sb_dtype, gate->group_size, ws + L.h,
+                      ws + L.y, x_dtype, ws + L.plan, L.h - L.plan);
+  if (up->sb_dtype != r.sb || down->sb_dtype != r.sb) return JQ_ERR_DTYPE;
+  r.logits = logits;
+  r.ro = ro;
+  r.cw = weights;
+  r.limit = limit;
+  r.before = before;
+  r.comb.shared_gate = shared_gate_logits;
+  r.comb.out = out;
+  r.comb.before = before;
+  if (has_shared) {
+    r.sg = shared_gate_proj;
+    r.su = shared_up_proj;
+    r.sd = shared_down_proj;
+    r.sI = shared_I;
+    r.sh_h = ws + L.sh_h;
+    r.sh_out = ws + L.sh_out;
+    // one token: the shared expert's gate|up runs inside the routed gate|up launch
+    if (fused_ok(r)) {
+      s = check_expert_shape(r.bits_gu, r.gs, E, I, H);
+      if (s) return s;
+      s = check_expert_shape(r.bits_d, r.gs, E, H, I);
+      if (s) return s;
+      if (H % 128 || I % 128) return JQ_ERR_SHAPE;
+      return moe_run_fused(r, st);
+    }
+  }
+  // Otherwise the shared expert first: its output joins the combine of the routed launch.
   void* sh_out = nullptr;
   if (has_shared) {
     const jq_qweight* sg = shared_gate_proj;
@@ -836,20 +937,9 @@ int jq_moe_block(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, in
                             x_dtype, stream);
     if (s) return s;
   }
-  MoeRun r = moe_args(x, x_dtype, T, H, I, E, idx, k, gate->codes, gate->scales, gate->biases,
-                      up->codes, up->scales, up->biases, gate->bits, down->codes, down->scales,
-                      down->biases, down->bits, gate->sb_dtype, gate->group_size, ws + L.h,
-                      ws + L.y, x_dtype, ws + L.plan, L.h - L.plan);
-  if (up->sb_dtype != r.sb || down->sb_dtype != r.sb) return JQ_ERR_DTYPE;
-  r.logits = logits;
-  r.ro = ro;
-  r.cw = weights;
-  r.limit = limit;
-  r.before = before;
+  r.sg = r.su = r.sd = nullptr;
+  r.sI = 0;
   r.comb.shared = sh_out;
-  r.comb.shared_gate = shared_gate_logits;
-  r.comb.out = out;
-  r.comb.before = before;
   return moe_run(r, st);
 }
 

@@ -237,4 +237,17 @@ int gemv_gather_route_launch(const QmmProblem& g, const QmmProblem& u, const Gat
                              int before, uint32_t* idx, float* w, int64_t T, int bits, int gs,
                              int xd, int sb, int yd, hipStream_t st);
 
+// The gate|up launch of one token's MoE block with the shared expert inside (jq_moe_fused.h):
+// the routed gate|up pairs of a launch that routes for itself and the shared expert's gate|up
+// rows (sg, su: [Is, H]) in one grid. bf16 activations and scales; routed bits 2..4 on rows of
+// at least 32 lane chunks, shared bits 4 or 8 on rows of at most two waves of chunks.
+// fused_rw: rows per wave instruction of a gathered projection with K inputs.
+int fused_rw(int64_t K, int bits);
+int moe_fused_gu_launch(const QmmProblem& g, const QmmProblem& u, const GatherPlan& plan,
+                        const void* logits, int64_t E, int k, const jqr::RouteOpts& ro,
+                        int before, uint32_t* idx, float* w, int bits_r, int gs_r,
+                        const QmvProblem& sg, const QmvProblem& su, int bits_s, int gs_s,
+                        float limit, hipStream_t st);
+
+
 }  // namespace jqk

@@ -82,8 +82,14 @@ def half_ulp(v: np.ndarray, dtype: str) -> np.ndarray:
     return np.ldexp(1.0, (e - mant).astype(np.int64))
 
 
+# Composite outputs (a MoE block, several bf16-rounded stages): rel-L2 bound. One ulp of
+# bf16 is 2^-8 relative; stages that flip an intermediate rounding move ~1 in 10-20 outputs
+# by one ulp, a rel-L2 of about 1e-3, so the bound is half an ulp of relative error.
+COMPOSITE_REL_L2_TOL = 2e-3
+
+
 def assert_close(got: np.ndarray, ref: np.ndarray, what: str,
-                 rel=REL_L2_TOL, mabs=MAX_ABS_TOL, exact=None, out_dtype=None, ulps=0.5):
+                 rel=None, mabs=MAX_ABS_TOL, exact=None, out_dtype=None, ulps=0.5):
     """rel-L2 of got against ref (the reference rounded to the output dtype) and max-abs
     error. With `exact` (the unrounded fp32/fp64 accumulation) the max-abs bound applies to
     |got - exact| beyond the output rounding itself (ulps = half an ulp of out_dtype): an
@@ -93,7 +99,12 @@ def assert_close(got: np.ndarray, ref: np.ndarray, what: str,
     activation dtype before the next stage, as the reference's arrays are) pass ulps=1: an
     intermediate value within fp32-vs-fp64 accumulation noise of a rounding midpoint may round
     the other way, and that one-ulp step moves every output of the next matmul slightly, so
-    some outputs legitimately land one ulp from the fp64 chain's rounding."""
+    some outputs legitimately land one ulp from the fp64 chain's rounding; their rel-L2
+    bound is COMPOSITE_REL_L2_TOL. Each stage alone is held to the north-star bounds by the
+    tests of its operator, and the fused launches are checked bit for bit against the
+    composition of those operators."""
+    if rel is None:
+        rel = COMPOSITE_REL_L2_TOL if ulps >= 1 else REL_L2_TOL
     r = O.rel_l2(got, ref)
     if exact is None:
         m = O.max_abs(got, ref)

@@ -7,7 +7,7 @@ import torch
 import jangq_amd as jq
 from jangq_amd import nn as jnn
 from oracle import jangq_oracle as O
-from tests._util import QWeight, assert_close, to_tensor, values_of
+from tests._util import QWeight, RandQ, assert_close, to_tensor, values_of
 
 pytestmark = pytest.mark.gpu
 
@@ -484,3 +484,58 @@ def test_moe_block_module_shared_gate(T):
         s_out = O.shared_expert(x[t], deqd["sg"], deqd["su"], deqd["sd"])
         ref, pre = O.moe_token(x[t], ids[t], w[t], deq, "after", 0.0, s_out, gl[t])
         assert_close(y[t], ref, f"gated block t{t}", exact=pre, out_dtype="bf16", ulps=1)
+
+
+@pytest.mark.parametrize("combine,limit,gated", [("after", 0.0, False), ("after", 0.4, True),
+                                                 ("before", 0.4, False)])
+@pytest.mark.parametrize("H,I,sI,bits,sbits,gs,E,k", [
+    (4096, 1024, 4096, 2, 8, 128, 64, 10),   # config-5 shapes: 2-bit g128 experts, 8-bit shared
+    (2048, 512, 2048, 3, 4, 64, 16, 4),      # 3-bit experts, 4-bit shared, one-wave rows
+])
+def test_moe_block_fused_decode(combine, limit, gated, H, I, sI, bits, sbits, gs, E, k):
+    """One token with a shared expert: the routed experts' gate|up (routing in the launch) and
+    the shared expert's gate|up share one launch. Checked against the oracle, and bit for bit
+    against the shared expert's own launches followed by jq_moe_experts (the same row and
+    gather bodies, the same reduction orders)."""
+    g = RandQ(I, H, bits, gs, seed=E + 1, experts=E)
+    u = RandQ(I, H, bits, gs, seed=E + 2, experts=E)
+    d = RandQ(H, I, bits, gs, seed=E + 3, experts=E)
+    sh = [RandQ(sI, H, sbits, 64, seed=E + 4), RandQ(sI, H, sbits, 64, seed=E + 5),
+          RandQ(H, sI, sbits, 64, seed=E + 6)]
+    rng = np.random.default_rng(H + k)
+    x = O.round_bf16(rng.standard_normal((1, H), dtype=np.float32))
+    logits = rng.standard_normal((1, E)).astype(np.float32)
+    gl = O.round_bf16(rng.standard_normal(1).astype(np.float32)) if gated else None
+    tx, tl = to_tensor(x, "bf16"), torch.from_numpy(logits).cuda()
+    tsh = tuple((q.dw, q.ds, q.db, 64, sbits) for q in sh)
+    out, ids, w = jq.moe_block(tx, tl, k, g.tup(), u.tup(), d.tup(), gs, shared=tsh,
+                               shared_gate=None if gl is None else to_tensor(gl, "bf16")[:, None],
+                               combine=combine, swiglu_limit=limit)
+    ridx, rw = O.route_topk(logits, k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ridx)
+    if combine == "after" and not gated and limit == 0.0:
+        hs = jq.quantized_swiglu(tx, (sh[0].dw, sh[0].ds, sh[0].db, sbits),
+                                 (sh[1].dw, sh[1].ds, sh[1].db, sbits), 64)
+        s_gpu = jq.quantized_matmul(hs, sh[2].dw, sh[2].ds, sh[2].db, True, 64, sbits)
+        out2, ids2, w2 = jq.moe_experts(tx, tl, k, g.tup(), u.tup(), d.tup(), gs, s_gpu)
+        assert torch.equal(ids, ids2) and torch.equal(w, w2)
+        assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), "fused != two-step"
+    cache = {}
+
+    def deq(c, e):
+        if (c, int(e)) not in cache:
+            ww, s_, b_ = {"g": g, "u": u, "d": d}[c].host(e)
+            cache[(c, int(e))] = O.dequantize_affine(ww, s_, b_, bits, gs).astype(np.float64)
+        return cache[(c, int(e))]
+
+    Ws = [O.dequantize_affine(*q.host(), sbits, 64).astype(np.float64) for q in sh]
+    s_out = O.shared_expert(x[0], *Ws, limit=limit)
+    ref, pre = O.moe_token(x[0], ridx[0], rw[0], deq, combine, limit, s_out,
+                           None if gl is None else gl[0])
+    assert_close(values_of(out)[0], ref, f"fused decode {combine} L{limit}", exact=pre,
+                 out_dtype="bf16", ulps=1)
+    # a second call gives the same bits
+    out3, _, _ = jq.moe_block(tx, tl, k, g.tup(), u.tup(), d.tup(), gs, shared=tsh,
+                              shared_gate=None if gl is None else to_tensor(gl, "bf16")[:, None],
+                              combine=combine, swiglu_limit=limit)
+    assert torch.equal(out3.view(torch.int16), out.view(torch.int16))
