@@ -178,6 +178,29 @@ int jq_mx_quantized_matmul(const void* x, int x_dtype, const uint32_t* codes,
                            void* y, int y_dtype, jq_stream_t stream);
 
 /*
+ * gather_qmm over MX-mode expert stacks (codes [E, N, K*mode/32], E8M0 scales uint8
+ * [E, N, K/32], no biases; format as jq_mx_dequantize): out[i*M + m] = x[lhs[i]*M + m] @
+ * W[rhs[i]]^T for pairs i < n_pairs and rows m < M (lhs NULL: i). x [x_batch, M, K] bf16/f16,
+ * out [n_pairs, M, N]; n_pairs * M < 65536. A pair whose expert id is >= E is not written.
+ * Replaces mx.gather_qmm(..., mode="mxfp4"/"mxfp8") as called from
+ * jang-tools/jang_tools/dots3/ops.py:181-188 on the expert stacks the loader switches to an
+ * MX mode (jang-tools/jang_tools/loader.py:1866-1912).
+ */
+int jq_mx_gather_qmm(const void* x, int x_dtype, int64_t x_batch, int64_t M,
+                     const uint32_t* codes, const uint8_t* scales, int mode, int64_t E,
+                     int64_t N, int64_t K, const uint32_t* lhs, const uint32_t* rhs,
+                     int64_t n_pairs, void* out, int y_dtype, jq_stream_t stream);
+
+/*
+ * Elementwise SwiGLU of two projections already rounded to dtype: h = round(silu(g) * u),
+ * with the clamp gate = min(g, L), up = clip(u, -L, L) when swiglu_limit > 0.
+ * No MLX operator as one call: silu(gate) * up of mlx_lm SwitchGLU (restated at
+ * jang-tools/jang_tools/dots3/ops.py:215) and jang-tools/jang_tools/dsv41/model.py:1214-1219.
+ */
+int jq_swiglu(const void* g, const void* u, int64_t n, float swiglu_limit, void* h, int dtype,
+              jq_stream_t stream);
+
+/*
  * Router: probs = softmax(logits) in fp32 (max-subtracted, "precise"), top-k expert ids
  * per token (ties -> lower id first), weights = their probabilities, optionally divided
  * by their sum (norm_topk_prob). logits f32 [T, E]; idx uint32 [T, k]; weights f32 [T, k].

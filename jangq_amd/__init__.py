@@ -20,6 +20,7 @@ from .ops import (  # noqa: F401
     quantized_swiglu,
     switch_glu,
     switch_glu_combine,
+    swiglu,
     unpack,
 )
 from ._lib import JangqError  # noqa: F401
@@ -27,6 +28,6 @@ from .shapes import bit_inference, infer_bits_group_size  # noqa: F401
 
 __all__ = [
     "dequantize", "dequantize_tensor", "expand_packed_1bit_to_2bit", "gather_qmm", "moe_block", "moe_combine", "moe_experts", "moe_route", "quantize", "quantized_matmul",
-    "quantized_matmul_multi", "quantized_swiglu", "switch_glu", "switch_glu_combine", "unpack", "bit_inference", "infer_bits_group_size",
+    "quantized_matmul_multi", "quantized_swiglu", "switch_glu", "switch_glu_combine", "swiglu", "unpack", "bit_inference", "infer_bits_group_size",
     "JangqError",
 ]

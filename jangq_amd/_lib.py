@@ -63,6 +63,8 @@ SIGNATURES = {
     ),
     "jq_quantized_matmul_noalloc": (_I, [_P, _I, _P, _P, _P, _I, _I, _I, _L, _L, _L, _P, _I, _P]),
     "jq_moe_route_ex": (_I, [_P, _I, _L, _L, _I, _P, _P, _P, _P]),
+    "jq_mx_gather_qmm": (_I, [_P, _I, _L, _L, _P, _P, _I, _L, _L, _L, _P, _P, _L, _P, _I, _P]),
+    "jq_swiglu": (_I, [_P, _P, _L, C.c_float, _P, _I, _P]),
     "jq_quantized_swiglu_ex": (
         _I,
         [_P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _P, _I, _I, _I, C.c_float, _P, _P, _I, _P],

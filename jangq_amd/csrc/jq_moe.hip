@@ -446,6 +446,19 @@ static int swiglu_run(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
   return jqh::launch_status();
 }
 
+int jq_swiglu(const void* g, const void* u, int64_t n, float swiglu_limit, void* h, int dtype,
+              jq_stream_t stream) {
+  if (n < 0 || !(swiglu_limit >= 0.f)) return JQ_ERR_SHAPE;
+  if (!jqh::dtype_ok(dtype)) return JQ_ERR_DTYPE;
+  if (n == 0) return JQ_OK;
+  if (!g || !u || !h) return JQ_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == JQ_BF16) swiglu_kernel<JQ_BF16><<<grid_for(n), 256, 0, st>>>(g, u, n, swiglu_limit, h);
+  else if (dtype == JQ_F16) swiglu_kernel<JQ_F16><<<grid_for(n), 256, 0, st>>>(g, u, n, swiglu_limit, h);
+  else swiglu_kernel<JQ_F32><<<grid_for(n), 256, 0, st>>>(g, u, n, swiglu_limit, h);
+  return jqh::launch_status();
+}
+
 int jq_quantized_swiglu(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
                         const uint32_t* gate_codes, const void* gate_scales,
                         const void* gate_biases, const uint32_t* up_codes, const void* up_scales,

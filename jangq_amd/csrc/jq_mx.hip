@@ -99,16 +99,36 @@ JQ_DEV float block_dot(const uint32_t* w, const uint32_t* xp, float part) {
 }
 
 // Rows per wave walk, blocks per lane XB (K <= 64 * 32 * XB), 4 waves per block.
+// Gathered form (MX expert stacks): blockIdx.y is (pair, activation row) p * M + m; the pair
+// reads x row lhs[p] * M + m (lhs NULL: p) and expert rhs[p]'s rows, and writes output row
+// p * M + m. A pair whose expert id is >= E writes nothing.
+struct MxGather {
+  const uint32_t* lhs;
+  const uint32_t* rhs;
+  int64_t M, E, x_rows;
+};
+
 template <int MODE, int XD, int XB>
 __global__ void __launch_bounds__(256) mx_gemv_kernel(const uint16_t* __restrict__ x,
                                                      const uint32_t* __restrict__ codes,
                                                      const uint8_t* __restrict__ scales,
                                                      int64_t N, int K, void* __restrict__ y,
-                                                     int yd, int rows_per_wave) {
+                                                     int yd, int rows_per_wave, MxGather gt) {
   constexpr int WPB = MODE == 4 ? 4 : 8;  // code words of a 32-element block
   const int lane = threadIdx.x & 63;
   const int wave = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
   const int nb = K / kMxBlock;  // blocks per row
+  if (gt.rhs) {
+    const int64_t pm = blockIdx.y, p = pm / gt.M, m = pm - p * gt.M;
+    const uint32_t e = gt.rhs[p];
+    if (e >= (uint32_t)gt.E) return;  // whole block
+    const int64_t xr = (gt.lhs ? (int64_t)gt.lhs[p] : p) * gt.M + m;
+    if (xr >= gt.x_rows) return;
+    x += xr * K;
+    codes += (int64_t)e * N * (K / (MODE == 4 ? 8 : 4));
+    scales += (int64_t)e * N * nb;
+    y = (char*)y + pm * N * (yd == JQ_F32 ? 4 : 2);
+  }
   // The lane's activations: XB blocks of 32 elements as 16 pairs each.
   uint32_t xa[XB][16];
 #pragma unroll
@@ -163,21 +183,22 @@ inline unsigned grid_for(int64_t n) {
 
 template <int MODE, int XD, int XB>
 void gemv_launch(const uint16_t* x, const uint32_t* codes, const uint8_t* scales, int64_t N,
-                 int K, void* y, int yd, hipStream_t st) {
+                 int K, void* y, int yd, const MxGather& gt, int64_t rows, hipStream_t st) {
   const int rpw = 2;
   const int64_t waves = (N + rpw - 1) / rpw;
-  mx_gemv_kernel<MODE, XD, XB><<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(
-      x, codes, scales, N, K, y, yd, rpw);
+  const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)rows);
+  mx_gemv_kernel<MODE, XD, XB><<<grid, 256, 0, st>>>(x, codes, scales, N, K, y, yd, rpw, gt);
 }
 
 template <int MODE, int XD>
 int gemv_xb(const uint16_t* x, const uint32_t* codes, const uint8_t* scales, int64_t N, int K,
-            void* y, int yd, hipStream_t st) {
+            void* y, int yd, hipStream_t st, const MxGather& gt = MxGather{nullptr, nullptr, 1, 0, 0},
+            int64_t rows = 1) {
   const int nb = K / kMxBlock;
-  if (nb <= 64) gemv_launch<MODE, XD, 1>(x, codes, scales, N, K, y, yd, st);
-  else if (nb <= 128) gemv_launch<MODE, XD, 2>(x, codes, scales, N, K, y, yd, st);
-  else if (nb <= 256) gemv_launch<MODE, XD, 4>(x, codes, scales, N, K, y, yd, st);
-  else gemv_launch<MODE, XD, 8>(x, codes, scales, N, K, y, yd, st);
+  if (nb <= 64) gemv_launch<MODE, XD, 1>(x, codes, scales, N, K, y, yd, gt, rows, st);
+  else if (nb <= 128) gemv_launch<MODE, XD, 2>(x, codes, scales, N, K, y, yd, gt, rows, st);
+  else if (nb <= 256) gemv_launch<MODE, XD, 4>(x, codes, scales, N, K, y, yd, gt, rows, st);
+  else gemv_launch<MODE, XD, 8>(x, codes, scales, N, K, y, yd, gt, rows, st);
   return jqh::launch_status();
 }
 
@@ -234,6 +255,31 @@ int jq_mx_quantized_matmul(const void* x, int x_dtype, const uint32_t* codes,
     if (s) return s;
   }
   return JQ_OK;
+}
+
+int jq_mx_gather_qmm(const void* x, int x_dtype, int64_t x_batch, int64_t M,
+                     const uint32_t* codes, const uint8_t* scales, int mode, int64_t E,
+                     int64_t N, int64_t K, const uint32_t* lhs, const uint32_t* rhs,
+                     int64_t n_pairs, void* out, int y_dtype, jq_stream_t stream) {
+  if (mode != 4 && mode != 8) return JQ_ERR_BITS;
+  if (K % kMxBlock) return JQ_ERR_GROUP_SIZE;
+  if (M <= 0 || N < 0 || K <= 0 || E <= 0 || x_batch < 0 || n_pairs < 0 ||
+      N >= ((int64_t)1 << 31) || K > 64 * kMxBlock * 8 || n_pairs * M >= 65536)
+    return JQ_ERR_SHAPE;
+  if (!lhs && x_batch < n_pairs) return JQ_ERR_SHAPE;
+  if (x_dtype != JQ_BF16 && x_dtype != JQ_F16) return JQ_ERR_DTYPE;
+  if (!jqh::dtype_ok(y_dtype)) return JQ_ERR_DTYPE;
+  if (n_pairs == 0 || N == 0) return JQ_OK;
+  if (!x || !codes || !scales || !rhs || !out) return JQ_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  const MxGather gt{lhs, rhs, M, E, x_batch * M};
+  const uint16_t* xs = (const uint16_t*)x;
+  const int64_t rows = n_pairs * M;
+  if (mode == 4)
+    return x_dtype == JQ_BF16 ? gemv_xb<4, JQ_BF16>(xs, codes, scales, N, (int)K, out, y_dtype, st, gt, rows)
+                              : gemv_xb<4, JQ_F16>(xs, codes, scales, N, (int)K, out, y_dtype, st, gt, rows);
+  return x_dtype == JQ_BF16 ? gemv_xb<8, JQ_BF16>(xs, codes, scales, N, (int)K, out, y_dtype, st, gt, rows)
+                            : gemv_xb<8, JQ_F16>(xs, codes, scales, N, (int)K, out, y_dtype, st, gt, rows);
 }
 
 }  // extern "C"

@@ -12,9 +12,13 @@ torch modules on the GPU:
     (affine.py:466-545); here the expansion runs on the GPU (``jq_expand_1bit_to_2bit``);
   - every quantized module's bits and group size are then fixed from its tensor shapes
     (``_fix_quantized_bits``, loader.py:1851-1982, through :func:`shapes.infer_bits_group_size`).
-A dense module whose scales are uint8 (E8M0) switches to the MX mode its shapes give, mxfp4
-or mxfp8 at group size 32, and drops the affine biases (loader.py:1877-1912); expert stacks
-in an MX mode raise (the gathered launches are affine only).
+A module whose scales are uint8 (E8M0), dense or an expert stack, switches to the MX mode its
+shapes give, mxfp4 or mxfp8 at group size 32, and drops the affine biases
+(loader.py:1877-1912). Float expert stacks (SwitchLinear) that the bundle holds quantized are
+upgraded to QuantizedSwitchLinear first (loader.py:1826-1848); a quantized gate loaded into a
+float router (DenseRouter) is dequantized to fp32 on the GPU (loader.py:452-482); and the
+reference's dtype policy (bfloat16 for 512+ experts at hidden 4096+, and for MLA models,
+loader.py:536-557) is applied to the floating tensors at the end.
 """
 from __future__ import annotations
 
@@ -42,6 +46,8 @@ class LoadReport:
     loaded: int = 0
     fixed: dict = field(default_factory=dict)
     expanded: list = field(default_factory=list)
+    upgraded: list = field(default_factory=list)
+    dtype: str | None = None
     unexpected: list = field(default_factory=list)
     missing: list = field(default_factory=list)
 
@@ -101,10 +107,7 @@ def _fix_bits(path: str, module, w_cols: int, s_cols: int) -> tuple[int, int]:
 
 def _load_mx(mod: str, m, w: torch.Tensor, s: torch.Tensor, device, report: LoadReport):
     """uint8 E8M0 scales: mxfp4 when 32 * scale columns == 8 * word columns, mxfp8 when
-    == 4 * word columns (loader.py:1877-1912); no biases."""
-    if isinstance(m, jnn.QuantizedSwitchLinear):
-        raise NotImplementedError(f"{mod}: MX-mode expert stacks are not implemented "
-                                  "(the gathered launches are affine only)")
+    == 4 * word columns (loader.py:1877-1912); no biases. Dense modules and expert stacks."""
     w_cols, s_cols = w.shape[-1], s.shape[-1]
     if s_cols * 32 == w_cols * 8:
         mode, bits = "mxfp4", 4
@@ -113,15 +116,78 @@ def _load_mx(mod: str, m, w: torch.Tensor, s: torch.Tensor, device, report: Load
     else:
         raise ValueError(f"{mod}: uint8 scales {tuple(s.shape)} fit no MX mode for weight "
                          f"{tuple(w.shape)}")
-    if s_cols * 32 != m.in_features or tuple(w.shape[:-1]) != tuple(m.weight.shape[:-1]):
+    in_f = getattr(m, "in_features", None) or getattr(m, "input_dims", None)
+    if s_cols * 32 != in_f or tuple(w.shape[:-1]) != tuple(m.weight.shape[:-1]):
         raise ValueError(f"{mod}: {mode} shapes {tuple(w.shape)} / {tuple(s.shape)} do not fit "
-                         f"the module ({m.out_features} x {m.in_features})")
+                         f"the module (rows {tuple(m.weight.shape[:-1])}, {in_f} inputs)")
     m.weight = w.view(torch.int32).to(device)
     m.scales = s.to(device)
     m.biases = None
     m.bits, m.group_size, m.mode = bits, 32, mode
     report.fixed[mod] = (mode, bits, 32)
     report.loaded += 2
+
+
+def dtype_policy(config: dict):
+    """The float dtype the reference loader forces on a model (loader.py:536-557): bfloat16 for
+    models with 512 or more experts and hidden size 4096 or more (float16 overflows at the
+    shared expert's down projection) and for MLA models (mistral4, kv_lora_rank > 0, whose
+    gate is dequantized to a float weight); None otherwise (stored dtypes kept)."""
+    text = config.get("text_config", config) or {}
+    n_exp = (text.get("num_experts") or text.get("num_local_experts")
+             or text.get("n_routed_experts") or 0)
+    if n_exp >= 512 and text.get("hidden_size", 0) >= 4096:
+        return torch.bfloat16
+    if text.get("model_type") == "mistral4" or (text.get("kv_lora_rank") or 0) > 0:
+        return torch.bfloat16
+    return None
+
+
+def _apply_dtype(model: torch.nn.Module, dtype) -> int:
+    """Cast every floating parameter and buffer of the model to dtype, the float32 router gate
+    included (MLX set_dtype's default predicate); codes and uint8 MX scales keep theirs.
+    Returns the number of tensors cast."""
+    n = 0
+    with torch.no_grad():
+        for mod in model.modules():
+            for name, t in list(mod._parameters.items()) + list(mod._buffers.items()):
+                if t is None or not t.is_floating_point() or t.dtype == dtype:
+                    continue
+                new = t.to(dtype)
+                if name in mod._parameters:
+                    mod._parameters[name] = torch.nn.Parameter(new, requires_grad=False)
+                else:
+                    mod._buffers[name] = new
+                n += 1
+    return n
+
+
+def _dequant_router(mod: str, m, t: dict, device, report: LoadReport):
+    """A quantized gate for a float router: dequantized on the GPU to fp32 with the first of
+    8, 6, 4, 3, 2 bits whose group size divides the row (loader.py:452-482). The reference
+    takes the first bits whose group size merely divides (so a 4-bit gs-64 gate also reads as
+    8-bit gs-32 at half its width); here the candidate must also give the router's input
+    width, which picks the one reading whose shape the model can use."""
+    w, s = t["weight"], t["scales"]
+    b = t.get("biases")
+    cols, scols = w.shape[-1], s.shape[-1]
+    if w.shape[0] != m.out_features:
+        raise ValueError(f"{mod}: gate rows {w.shape[0]} != {m.out_features} experts")
+    for bits in (8, 6, 4, 3, 2):
+        real = cols * 32 // bits
+        gs = real // scols if scols else 0
+        if gs in (32, 64, 128) and gs * scols == real and real == m.in_features:
+            break
+    else:
+        raise ValueError(f"{mod}: quantized gate {tuple(w.shape)} / {tuple(s.shape)} fits no "
+                         f"bits / group size for {m.in_features} inputs")
+    s = s.to(device)
+    b = torch.zeros_like(s) if b is None else b.to(device)
+    dq = ops.dequantize(w.view(torch.int32).to(device), s, b, gs, bits, dtype=torch.float32)
+    with torch.no_grad():
+        m.weight = torch.nn.Parameter(dq, requires_grad=False)
+    report.fixed[mod] = ("dequantized", bits, gs)
+    report.loaded += 3
 
 
 def load_bundle_into(model: torch.nn.Module, path, *, device=None,
@@ -131,26 +197,44 @@ def load_bundle_into(model: torch.nn.Module, path, *, device=None,
     the device of the model's first tensor). Codes stay uint32 words (held as int32), scales
     and biases keep their stored dtype. With ``strict`` a key that matches nothing, or a
     module tensor the bundle lacks, raises KeyError."""
-    _, jang = read_configs(path)
+    cfg, jang = read_configs(path)
     one_bit = affine1_modules(jang)
     if device is None:
         first = next(iter(model.state_dict().values()), None)
         device = first.device if first is not None else torch.device("cpu")
     device = torch.device(device)
+    report = LoadReport()
+
+    from safetensors import safe_open
+
+    keys = {}
+    for shard in shard_paths(path):
+        with safe_open(str(shard), framework="pt") as f:
+            for key in f.keys():
+                keys[key] = shard
+    # Float expert stacks the bundle holds quantized become QuantizedSwitchLinear
+    # (loader.py:1826-1848); their bits and group size are fixed below from the shapes.
+    q = cfg.get("quantization") or {}
+    upgrade = {n for n, m in model.named_modules()
+               if isinstance(m, jnn.SwitchLinear) and f"{n}.scales" in keys}
+    if upgrade:
+        report.upgraded = jnn.upgrade_switch_to_quantized(
+            model, int(q.get("bits", 4)), int(q.get("group_size", 64)), names=upgrade)
     modules = dict(model.named_modules())
     quant = {n: m for n, m in modules.items()
              if isinstance(m, (jnn.QuantizedLinear, jnn.QuantizedSwitchLinear))}
+    routers = {n: m for n, m in modules.items() if isinstance(m, jnn.DenseRouter)}
     state = model.state_dict()
-    report = LoadReport()
     pending: dict[str, dict] = {}
-
-    from safetensors import safe_open
+    gates: dict[str, dict] = {}
 
     for shard in shard_paths(path):
         with safe_open(str(shard), framework="pt") as f:
             for key in f.keys():
                 mod, attr = _split(key)
-                if mod in quant and attr in _QUANT_ATTRS:
+                if mod in routers and attr in _QUANT_ATTRS and f"{mod}.scales" in keys:
+                    gates.setdefault(mod, {})[attr] = f.get_tensor(key)
+                elif mod in quant and attr in _QUANT_ATTRS:
                     pending.setdefault(mod, {})[attr] = f.get_tensor(key)
                 elif key in state:
                     t = f.get_tensor(key)
@@ -205,9 +289,16 @@ def load_bundle_into(model: torch.nn.Module, path, *, device=None,
         m.bits, m.group_size, m.mode = bits, gs, "affine"
         report.loaded += 3
 
+    for mod, t in gates.items():
+        _dequant_router(mod, routers[mod], t, device, report)
+
     for mod in quant:
         if mod not in pending:
             report.missing += [f"{mod}.{a}" for a in _QUANT_ATTRS]
+    dt = dtype_policy(cfg)
+    if dt is not None:
+        report.dtype = str(dt).replace("torch.", "")
+        _apply_dtype(model, dt)
     if strict and (report.unexpected or report.missing):
         raise KeyError(f"bundle/module mismatch: unexpected {report.unexpected[:8]}, "
                        f"missing {report.missing[:8]}")

@@ -4,11 +4,16 @@
   QuantizedSwitchLinear          mlx_lm switch_layers, as upgraded by loader.py:1826-1848;
                                  the DSV4.1 SwitchProj (dsv41/model.py:847-857) has the same call
   SwitchGLU                      mlx_lm SwitchGLU (restated at dots3/ops.py:195-223)
+  SwitchLinear                   mlx_lm SwitchLinear (float experts), upgraded to
+                                 QuantizedSwitchLinear by loader.py:1826-1848
+  DenseRouter                    the float MoEGate of mistral4_mlx.py:343-352
   SparseMoeBlock                 qwen4_exp/modeling.py:577-599 routing + experts + shared expert
 Parameters are plain tensors (weight uint32, scales/biases bf16 by default) that a loader
 fills; every forward runs the gfx950 kernels through :mod:`jangq_amd.ops`.
 """
 from __future__ import annotations
+
+import math
 
 import torch
 
@@ -76,7 +81,7 @@ class QuantizedSwitchLinear(torch.nn.Module):
                 sorted_indices: bool = False) -> torch.Tensor:
         y = ops.gather_qmm(x, self.weight, self.scales, self.biases, rhs_indices=indices,
                            transpose=True, group_size=self.group_size, bits=self.bits,
-                           sorted_indices=sorted_indices)
+                           mode=self.mode, sorted_indices=sorted_indices)
         if self.bias is not None:
             y = y + self.bias[indices.long()].unsqueeze(-2)
         return y
@@ -105,9 +110,86 @@ class SwitchGLU(torch.nn.Module):
             raise ValueError(f"SwitchGLU projections have different group sizes {sorted(gs)}")
         return self.gate_proj.group_size
 
-    def forward(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
-        return ops.switch_glu(x, indices, self.gate_proj.as_tuple(), self.up_proj.as_tuple(),
-                              self.down_proj.as_tuple(), self.group_size())
+    def is_affine(self) -> bool:
+        return all(p.mode == "affine" for p in (self.gate_proj, self.up_proj, self.down_proj))
+
+    def forward(self, x: torch.Tensor, indices: torch.Tensor,
+                swiglu_limit: float = 0.0) -> torch.Tensor:
+        if self.is_affine() and swiglu_limit == 0.0:
+            return ops.switch_glu(x, indices, self.gate_proj.as_tuple(), self.up_proj.as_tuple(),
+                                  self.down_proj.as_tuple(), self.group_size())
+        # MX-mode stacks (or a clamp): the three gathers of mlx_lm SwitchGLU (restated at
+        # dots3/ops.py:195-223) with the elementwise SwiGLU between them
+        xe = x.reshape(*x.shape[:-1], 1, 1, x.shape[-1])
+        g = self.gate_proj(xe, indices)
+        u = self.up_proj(xe, indices)
+        h = ops.swiglu(g, u, swiglu_limit)
+        return self.down_proj(h, indices).squeeze(-2)
+
+
+class SwitchLinear(torch.nn.Module):
+    """Float stacked-expert projection (mlx_lm SwitchLinear): x @ weight[indices]^T. A bundle
+    that holds quantized tensors for it upgrades it to QuantizedSwitchLinear
+    (:func:`upgrade_switch_to_quantized`, loader.py:1826-1848)."""
+
+    def __init__(self, input_dims: int, output_dims: int, num_experts: int, bias: bool = False,
+                 *, dtype=torch.bfloat16, device=None):
+        super().__init__()
+        self.input_dims, self.output_dims, self.num_experts = input_dims, output_dims, num_experts
+        self.weight = torch.nn.Parameter(torch.zeros((num_experts, output_dims, input_dims),
+                                                     dtype=dtype, device=device),
+                                         requires_grad=False)
+        self.bias = (torch.nn.Parameter(torch.zeros((num_experts, output_dims), dtype=dtype,
+                                                    device=device), requires_grad=False)
+                     if bias else None)
+
+    def forward(self, x: torch.Tensor, indices: torch.Tensor,
+                sorted_indices: bool = False) -> torch.Tensor:
+        # x [..., M, K] broadcast against indices as gather_qmm does; fp32 products
+        bshape = x.shape[:-2]
+        lhs = torch.arange(math.prod(bshape), device=x.device).reshape(bshape)
+        lhs_b, rhs_b = torch.broadcast_tensors(lhs, indices.long())
+        xs = x.reshape(-1, *x.shape[-2:])[lhs_b.reshape(-1)].float()
+        w = self.weight[rhs_b.reshape(-1)].float().transpose(-1, -2).contiguous()
+        y = torch.matmul(xs, w)
+        if self.bias is not None:
+            y = y + self.bias[rhs_b.reshape(-1)].float().unsqueeze(-2)
+        return y.to(x.dtype).reshape(*lhs_b.shape, *y.shape[-2:])
+
+
+def upgrade_switch_to_quantized(model: torch.nn.Module, bits: int, group_size: int,
+                                names=None) -> list:
+    """Replace SwitchLinear modules (all, or those in ``names``) with QuantizedSwitchLinear of
+    the same dimensions (jang-tools/jang_tools/loader.py:1826-1848). Returns the paths."""
+    done = []
+    for name, mod in list(model.named_modules()):
+        if not isinstance(mod, SwitchLinear) or (names is not None and name not in names):
+            continue
+        q = QuantizedSwitchLinear(mod.input_dims, mod.output_dims, mod.num_experts,
+                                  bias=mod.bias is not None, group_size=group_size, bits=bits,
+                                  device=mod.weight.device)
+        parent_name, _, leaf = name.rpartition(".")
+        parent = model.get_submodule(parent_name) if parent_name else model
+        setattr(parent, leaf, q)
+        done.append(name)
+    return done
+
+
+class DenseRouter(torch.nn.Module):
+    """A MoE router kept in floating point (mistral4_mlx.py:343-352 MoEGate: the gate stays
+    float; the loader dequantizes a quantized gate into it, loader.py:452-482): logits =
+    x @ weight^T accumulated in fp32 and returned in the promoted type of x and the weight
+    (float32 for a float32 gate, bfloat16 once the loader's dtype policy casts both)."""
+
+    def __init__(self, dims: int, num_experts: int, *, dtype=torch.float32, device=None):
+        super().__init__()
+        self.in_features, self.out_features = dims, num_experts
+        self.weight = torch.nn.Parameter(torch.zeros((num_experts, dims), dtype=dtype,
+                                                     device=device), requires_grad=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        out = torch.matmul(x.float(), self.weight.float().t().contiguous())
+        return out.to(torch.promote_types(x.dtype, self.weight.dtype))
 
 
 class SharedExpertMLP(torch.nn.Module):
@@ -196,6 +278,16 @@ class SparseMoeBlock(torch.nn.Module):
             logits = self.gate(x)  # the router's bf16/f16 output is read as it is
         sgl = self.shared_expert_gate(x) if self.shared_expert_gate is not None else None
         m = self.switch_mlp
+        if not m.is_affine():
+            # MX-mode experts: routing, the three gathers and the combine as separate launches
+            if self.combine != "after" or sgl is not None:
+                raise NotImplementedError("MX-mode experts take the after-down combine without "
+                                          "a shared-expert gate")
+            kw = self._route_kw()
+            idx, w = ops.moe_route(logits, self.top_k, kw.pop("renorm"), **kw)
+            y = m(x, idx, self.swiglu_limit)
+            shared = self.shared_expert(x) if self.shared_expert is not None else None
+            return ops.moe_combine(y, w, shared)
         # routing, the routed experts, the shared expert and the combine in one call; at decode
         # sizes the routed experts take two launches (gate|up routing for itself, then down
         # with the combine inside).

@@ -323,7 +323,7 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     Output [*broadcast(lhs, rhs), M, N] in x.dtype."""
     _check_mode(mode, transpose)
     if mode in MX_MODES:
-        raise ValueError(f"gather_qmm: mode={mode!r} is not implemented (affine only)")
+        return _mx_gather(x, w, scales, lhs_indices, rhs_indices, group_size, bits, mode)
     _check_bits_gs(bits, group_size)
     x = _dev(x, "x")
     w = _codes(w)
@@ -382,6 +382,47 @@ def _route_opts(score: str, renorm: bool, renorm_eps: float | None, scaling: flo
     o = _lib.RouteOpts(_lib.JQ_SCORE[score], int(bool(renorm)), eps, float(scaling), bias_ptr,
                        max(int(n_group), 1), int(topk_group))
     return o, keep
+
+
+def _mx_gather(x, w, scales, lhs_indices, rhs_indices, group_size, bits, mode):
+    """gather_qmm over an MX-mode expert stack (no biases): one gathered GEMV launch per call,
+    every (pair, activation row) its own row of the grid."""
+    w, scales, K = _mx_check(w, scales, group_size, bits, mode)
+    x = _dev(x, "x")
+    if w.dim() != 3 or x.dim() < 2 or x.shape[-1] != K:
+        raise ValueError(f"MX gather_qmm: x {tuple(x.shape)} / w {tuple(w.shape)} do not match")
+    E, N = w.shape[0], w.shape[1]
+    M = x.shape[-2]
+    bshape = tuple(x.shape[:-2])
+    Bx = math.prod(bshape)
+    dev = x.device
+    if lhs_indices is None:
+        lhs_indices = torch.arange(Bx, device=dev, dtype=torch.int32).reshape(bshape)
+    if rhs_indices is None:
+        rhs_indices = torch.arange(E, device=dev, dtype=torch.int32)
+    lhs_b, rhs_b = torch.broadcast_tensors(lhs_indices.to(dev), rhs_indices.to(dev))
+    ishape = tuple(lhs_b.shape)
+    lhs_f = lhs_b.reshape(-1).to(torch.int32).contiguous()
+    rhs_f = rhs_b.reshape(-1).to(torch.int32).contiguous()
+    n = lhs_f.numel()
+    out = torch.empty((*ishape, M, N), dtype=x.dtype, device=dev)
+    if n == 0:
+        return out
+    _lib.check(_lib.lib().jq_mx_gather_qmm(
+        _ptr(x), _dtype_code(x, "x"), Bx, M, _ptr(w), _ptr(scales), bits, E, N, K, _ptr(lhs_f),
+        _ptr(rhs_f), n, _ptr(out), _dtype_code(out, "output"), _stream()), "gather_qmm")
+    return out
+
+
+def swiglu(g: torch.Tensor, u: torch.Tensor, swiglu_limit: float = 0.0) -> torch.Tensor:
+    """round(silu(g) * u) elementwise (g, u already in their dtype), with the optional clamp."""
+    g, u = _dev(g, "g"), _dev(u, "u")
+    if g.shape != u.shape or g.dtype != u.dtype:
+        raise ValueError("g and u must share shape and dtype")
+    h = torch.empty_like(g)
+    _lib.check(_lib.lib().jq_swiglu(_ptr(g), _ptr(u), g.numel(), float(swiglu_limit), _ptr(h),
+                                    _dtype_code(g, "g"), _stream()), "swiglu")
+    return h
 
 
 def moe_route(logits: torch.Tensor, k: int, renorm: bool = True, *, score: str = "softmax",

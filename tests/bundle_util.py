@@ -32,7 +32,7 @@ def tensors_of(prefix, packed, s, b, sidecar="bf16"):
 
 
 def write_bundle(root, tensors: dict, *, bits=2, group_size=64, manifest=None, shards=2,
-                 fmt="jang", version="2.0"):
+                 fmt="jang", version="2.0", config_extra=None):
     root = Path(root)
     root.mkdir(parents=True, exist_ok=True)
     keys = sorted(tensors)
@@ -40,8 +40,9 @@ def write_bundle(root, tensors: dict, *, bits=2, group_size=64, manifest=None, s
         part = {k: tensors[k].contiguous() for k in keys[i::shards]}
         if part:
             save_file(part, str(root / f"model-{i + 1:05d}-of-{shards:05d}.safetensors"))
-    (root / "config.json").write_text(json.dumps(
-        {"model_type": "synthetic_moe", "quantization": {"group_size": group_size, "bits": bits}}))
+    cfg = {"model_type": "synthetic_moe", "quantization": {"group_size": group_size, "bits": bits}}
+    cfg.update(config_extra or {})
+    (root / "config.json").write_text(json.dumps(cfg))
     q = {"profile": "JANG_2L", "block_size": group_size, "bit_widths_used": [2, 8]}
     if manifest:
         q["tensor_quantization_manifest"] = manifest

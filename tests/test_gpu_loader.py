@@ -73,3 +73,62 @@ def test_loaded_block_matches_oracle(tmp_path):
     h = O.round_bf16(O.silu(g) * u)
     shared = O.round_bf16(O.quantized_matmul(h, *sd, 8, 64))
     assert_close(values_of(y), O.round_bf16(routed + shared), "loaded moe block")
+
+
+class _RouterModel(torch.nn.Module):
+    def __init__(self, experts, dims):
+        super().__init__()
+        self.gate = jnn.DenseRouter(dims, experts, device="cuda")
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 64), (8, 32), (3, 128)])
+def test_quantized_gate_into_float_router(tmp_path, bits, gs):
+    """A quantized gate loaded into a float router is dequantized to fp32 (loader.py:452-482),
+    bit-exact to the oracle's dequantization; the router's logits follow in fp32."""
+    Ex, D = 16, 512
+    p, s, b = quantized(Ex, D, bits, gs, 40 + bits)
+    write_bundle(tmp_path, tensors_of("gate", p, s, b))
+    m = _RouterModel(Ex, D)
+    rep = loader.load_bundle_into(m, tmp_path)
+    assert rep.fixed["gate"] == ("dequantized", bits, gs) and not rep.unexpected
+    ref = O.dequantize_affine(p, O.sidecar_f32(s, "bf16"), O.sidecar_f32(b, "bf16"), bits, gs)
+    assert m.gate.weight.dtype == torch.float32
+    np.testing.assert_array_equal(m.gate.weight.cpu().numpy(), ref.astype(np.float32))
+    x = O.round_bf16(np.random.default_rng(1).standard_normal((3, D), dtype=np.float32))
+    y = m.gate(to_tensor(x, "bf16"))
+    assert y.dtype == torch.float32
+    exact = x.astype(np.float64) @ ref.astype(np.float64).T
+    np.testing.assert_allclose(values_of(y), exact, rtol=1e-4, atol=1e-4)
+
+
+def test_mx_expert_stack_loaded_and_run(tmp_path):
+    """An mxfp4 expert stack in a bundle loads onto the block's SwitchGLU (mode, bits and group
+    size from the shapes, no biases) and the loaded experts run the MX gathers."""
+    rng = np.random.default_rng(21)
+    t = {}
+    t.update(tensors_of("gate", *quantized(E, H, 8, 64, 1)))
+    host = {}
+    for name, (n, kk) in {"gate_proj": (I, H), "up_proj": (I, H), "down_proj": (H, I)}.items():
+        packed = rng.integers(0, 2**32, (E, n, kk // 8), dtype=np.uint64).astype(np.uint32)
+        sc = rng.integers(112, 122, (E, n, kk // 32)).astype(np.uint8)
+        host[name] = (packed, sc)
+        t[f"switch_mlp.{name}.weight"] = torch.from_numpy(packed.view(np.int32)).view(torch.uint32)
+        t[f"switch_mlp.{name}.scales"] = torch.from_numpy(sc)
+    write_bundle(tmp_path, t)
+    blk = jnn.SparseMoeBlock(H, I, E, K_TOP, group_size=64, bits=2, router_bits=8, device="cuda")
+    rep = loader.load_bundle_into(blk, tmp_path)
+    assert all(rep.fixed[f"switch_mlp.{n}"] == ("mxfp4", 4, 32)
+               for n in ("gate_proj", "up_proj", "down_proj"))
+    x = O.round_bf16(rng.standard_normal((2, H), dtype=np.float32))
+    idx = np.array([[1, 5], [7, 0]], dtype=np.int32)
+    y = blk.switch_mlp(to_tensor(x, "bf16"), torch.from_numpy(idx).cuda())
+    exact = np.zeros((2, K_TOP, H))
+    for t_ in range(2):
+        for j in range(K_TOP):
+            e = idx[t_, j]
+            mm = lambda v, nm: O.mx_quantized_matmul(v, host[nm][0][e], host[nm][1][e], "mxfp4")
+            g = O.round_bf16(mm(x[t_:t_ + 1], "gate_proj"))
+            u = O.round_bf16(mm(x[t_:t_ + 1], "up_proj"))
+            exact[t_, j] = mm(O.round_bf16(O.glu(g, u)), "down_proj")[0]
+    assert_close(values_of(y), O.round_bf16(exact), "loaded mx experts", exact=exact,
+                 out_dtype="bf16", ulps=1)
