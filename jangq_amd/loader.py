@@ -30,6 +30,7 @@ import torch
 
 from . import nn as jnn
 from . import ops
+from . import shards
 from .shapes import infer_bits_group_size, is_router_name
 
 AFFINE1_STORAGE_BITS = 1
@@ -190,6 +191,36 @@ def _dequant_router(mod: str, m, t: dict, device, report: LoadReport):
     report.loaded += 3
 
 
+class _Views:
+    """get_tensor over the zero-copy views of an aligned shard (context-manager form of
+    safe_open)."""
+
+    def __init__(self, shard):
+        self.v = shards.open_views(shard)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        return False
+
+    def keys(self):
+        return self.v.keys()
+
+    def get_tensor(self, key):
+        return self.v[key]
+
+
+def _open_shard(shard, device):
+    """A GPU load of a dtype-aligned shard reads the tensors as views of the mapped file, so
+    each upload copies straight from the page cache; other shards (and CPU loads, whose
+    tensors must not alias a read-only mapping) go through safetensors' own reader."""
+    from safetensors import safe_open
+    if device.type == "cuda" and shards.verify_alignment(shard)[1] == 0:
+        return _Views(shard)
+    return safe_open(str(shard), framework="pt")
+
+
 def load_bundle_into(model: torch.nn.Module, path, *, device=None,
                      strict: bool = False) -> LoadReport:
     """Assign a v2 bundle's tensors to ``model``'s quantized modules (QuantizedLinear,
@@ -229,7 +260,7 @@ def load_bundle_into(model: torch.nn.Module, path, *, device=None,
     gates: dict[str, dict] = {}
 
     for shard in shard_paths(path):
-        with safe_open(str(shard), framework="pt") as f:
+        with _open_shard(shard, device) as f:
             for key in f.keys():
                 mod, attr = _split(key)
                 if mod in routers and attr in _QUANT_ATTRS and f"{mod}.scales" in keys:

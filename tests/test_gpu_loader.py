@@ -132,3 +132,29 @@ def test_mx_expert_stack_loaded_and_run(tmp_path):
             exact[t_, j] = mm(O.round_bf16(O.glu(g, u)), "down_proj")[0]
     assert_close(values_of(y), O.round_bf16(exact), "loaded mx experts", exact=exact,
                  out_dtype="bf16", ulps=1)
+
+
+def test_aligned_bundle_loads_the_same(tmp_path):
+    """The same bundle repacked into dtype-aligned shards (read as views of the mapped files)
+    loads tensors identical to the original's (read through safetensors)."""
+    from jangq_amd import shards
+    t = {}
+    t.update(tensors_of("gate", *quantized(E, H, 8, 64, 1)))
+    t.update(tensors_of("switch_mlp.gate_proj", *quantized(I, H, 3, 128, 2, experts=E)))
+    t.update(tensors_of("switch_mlp.up_proj", *quantized(I, H, 3, 128, 3, experts=E)))
+    t.update(tensors_of("switch_mlp.down_proj", *quantized(H, I, 4, 64, 4, experts=E)))
+    t["norm.odd"] = torch.ones(3, dtype=torch.bfloat16)  # 6 bytes: misaligns what follows
+    write_bundle(tmp_path / "src", t)
+    shards.repack_bundle(tmp_path / "src", tmp_path / "al")
+    for p in (tmp_path / "al").glob("*.safetensors"):
+        assert shards.verify_alignment(p)[1] == 0
+    mk = lambda: jnn.SparseMoeBlock(H, I, E, K_TOP, group_size=64, bits=2, router_bits=8,
+                                    device="cuda")
+    a, b = mk(), mk()
+    ra = loader.load_bundle_into(a, tmp_path / "src")
+    rb = loader.load_bundle_into(b, tmp_path / "al")
+    assert ra.fixed == rb.fixed and ra.loaded == rb.loaded and ra.unexpected == rb.unexpected
+    sa, sb = a.state_dict(), b.state_dict()
+    assert sa.keys() == sb.keys()
+    for k in sa:
+        assert sa[k].device.type == "cuda" and torch.equal(sa[k], sb[k]), k
