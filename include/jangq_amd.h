@@ -104,7 +104,9 @@ int jq_expand_1bit_to_2bit(const uint32_t* src, int64_t words, uint32_t* dst,
  * Replaces mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits) as
  * called from jang-tools/jang_tools/jangrt/linear.py:41-45 and
  * jang-tools/jang_tools/dots3/ops.py:44-51. Small M runs the decode GEMV kernels, larger
- * M the matrix-core GEMM.
+ * M the matrix-core GEMM; from 384 rows the f16 prefill GEMM, whose f16 activation copy this
+ * entry point takes from a stream-ordered allocation (hipMallocAsync / hipFreeAsync on
+ * `stream`; jq_quantized_matmul_ws takes it from the caller instead).
  */
 int jq_quantized_matmul(const void* x, int x_dtype, const uint32_t* codes,
                         const void* scales, const void* biases, int sb_dtype, int bits,
@@ -114,10 +116,13 @@ int jq_quantized_matmul(const void* x, int x_dtype, const uint32_t* codes,
 /*
  * jq_quantized_matmul with a caller workspace (same reference call: mx.quantized_matmul at
  * jang-tools/jang_tools/jangrt/linear.py:41-45). Decode batches of long rows (5..64 rows,
- * K > 4096) split K over the matrix-core kernel and sum fp32 partials in the workspace;
- * every other shape runs exactly as jq_quantized_matmul. The size query returns the bytes
- * needed (0: no workspace used, -1: invalid sizes); a smaller workspace returns
- * JQ_ERR_WORKSPACE.
+ * K > 4096) split K over the matrix-core kernel and sum fp32 partials in the workspace
+ * (a smaller workspace returns JQ_ERR_WORKSPACE). Prefill shapes (384 rows and more, group
+ * size 64 or 128) hold their activations as f16 rows in the workspace (M*K*2 bytes plus
+ * 4 bytes per row of x and of W); a smaller workspace runs the rows in passes of whole
+ * 256-row tiles, and one below 256 rows' worth returns JQ_ERR_WORKSPACE. Every other shape
+ * runs exactly as jq_quantized_matmul. The size query returns the bytes for one pass (0: no
+ * workspace used, -1: invalid sizes).
  */
 int64_t jq_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int bits,
                                            int group_size, int x_dtype, int sb_dtype);
@@ -130,11 +135,12 @@ int jq_quantized_matmul_ws(const void* x, int x_dtype, const uint32_t* codes,
 /*
  * jq_quantized_matmul_ws without a workspace argument, for callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops, harnesses that forbid it); it has no
- * counterpart in the reference. The K-split partials of decode batches of long rows go to a
- * fixed array inside the library, JQ_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on
- * a GPU until the process ends; a shape that needs more returns JQ_ERR_WORKSPACE (the size
- * query jq_quantized_matmul_workspace_size tells it beforehand). Every other shape runs as
- * jq_quantized_matmul. It calls no allocator. Calls that overlap on one GPU (other streams or
+ * counterpart in the reference. The K-split partials of decode batches of long rows and the
+ * prefill GEMM's f16 activation rows go to a fixed array inside the library,
+ * JQ_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on a GPU until the process ends;
+ * a K-split shape that needs more returns JQ_ERR_WORKSPACE (the size query
+ * jq_quantized_matmul_workspace_size tells it beforehand), a prefill shape runs in passes of
+ * rows that fit. Every other shape runs as jq_quantized_matmul. It calls no allocator. Calls that overlap on one GPU (other streams or
  * threads) share the array and race; the array keeps the last call's contents, and each call
  * writes every partial it reads.
  */

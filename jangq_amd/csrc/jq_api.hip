@@ -20,6 +20,30 @@ constexpr int64_t kDecpMaxRows = 64;
 constexpr int64_t kQmv4MinK = 8192;
 inline bool use_qmv4(int64_t M, int64_t K) { return M <= kDecpMaxRows && K >= kQmv4MinK; }
 
+inline bool al(const void* p, uintptr_t n) { return ((uintptr_t)p & (n - 1)) == 0; }
+
+// The f16 prefill GEMM takes large-M shapes whose operands it can copy in whole dwords
+// (activation rows in 16-byte pieces); it needs a workspace for the f16 activations.
+inline bool gemm16_shape(int64_t M, int64_t K, int bits, int gs, int xd, int sb) {
+  return M >= kGemmMinRows && jqk::gemm16_ok(M, K, bits, gs, xd, sb);
+}
+inline bool use_gemm16(const void* x, const uint32_t* codes, const void* scales,
+                       const void* biases, int64_t M, int64_t K, int bits, int gs, int xd,
+                       int sb) {
+  return gemm16_shape(M, K, bits, gs, xd, sb) && al(x, 16) && al(codes, 4) && al(scales, 4) &&
+         al(biases, 4);
+}
+
+jqk::QmmProblem dense_problem(const void* x, const uint32_t* codes, const void* scales,
+                              const void* biases, int64_t M, int64_t N, int64_t K, void* y) {
+  jqk::QmmProblem p;
+  p.x = x; p.codes = codes; p.scales = scales; p.biases = biases; p.y = y;
+  p.M = M; p.N = N; p.K = K;
+  p.expert_stride_codes = 0;
+  p.expert_stride_sb = 0;
+  return p;
+}
+
 int dense_one(const void* x, int xd, const uint32_t* codes, const void* scales,
               const void* biases, int sb, int bits, int gs, int64_t M, int64_t N, int64_t K,
               void* y, int yd, hipStream_t st) {
@@ -56,6 +80,18 @@ int dense_one(const void* x, int xd, const uint32_t* codes, const void* scales,
     b.p[0].x = x; b.p[0].codes = codes; b.p[0].scales = scales; b.p[0].biases = biases;
     b.p[0].y = y; b.p[0].N = N;
     return jqk::decp_launch(b, 1, bits, gs, xd, sb, yd, st);
+  }
+  if (use_gemm16(x, codes, scales, biases, M, K, bits, gs, xd, sb)) {
+    // No caller workspace here: a stream-ordered allocation for the f16 activations.
+    const int64_t need = jqk::gemm16_workspace(M, N, K, gs);
+    void* ws = nullptr;
+    if (hipMallocAsync(&ws, (size_t)need, st) == hipSuccess) {
+      const int s = jqk::gemm16_launch(dense_problem(x, codes, scales, biases, M, N, K, y), bits,
+                                       gs, xd, sb, yd, ws, need, st);
+      const hipError_t f = hipFreeAsync(ws, st);
+      return s ? s : (f == hipSuccess ? JQ_OK : JQ_ERR_LAUNCH);
+    }
+    (void)hipGetLastError();  // out of memory: the workspace-free GEMM below
   }
   if (M >= kGemmMinRows && jqk::gemm_ok(M, K, bits, gs, xd, sb)) {
     jqk::QmmProblem p;
@@ -144,6 +180,8 @@ static bool use_split(int64_t M, int64_t N, int64_t K, int bits, int gs, int xd,
 int64_t jq_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int bits,
                                            int group_size, int x_dtype, int sb_dtype) {
   if (M < 0 || N < 0 || K < 0) return -1;
+  if (M > 0 && N > 0 && gemm16_shape(M, K, bits, group_size, x_dtype, sb_dtype))
+    return jqk::gemm16_workspace(M, N, K, group_size);
   if (!use_split(M, N, K, bits, group_size, x_dtype, sb_dtype)) return 0;
   return jqk::dmx_split_workspace((int)M, K, N, bits, group_size, x_dtype, sb_dtype);
 }
@@ -155,6 +193,11 @@ int jq_quantized_matmul_ws(const void* x, int x_dtype, const uint32_t* codes, co
   int s = check_dense(x, x_dtype, codes, scales, biases, sb_dtype, bits, group_size, M, N, K, y,
                       y_dtype);
   if (s) return s;
+  if (M > 0 && N > 0 && K > 0 &&
+      use_gemm16(x, codes, scales, biases, M, K, bits, group_size, x_dtype, sb_dtype))
+    return jqk::gemm16_launch(dense_problem(x, codes, scales, biases, M, N, K, y), bits,
+                              group_size, x_dtype, sb_dtype, y_dtype, workspace, workspace_bytes,
+                              (hipStream_t)stream);
   if (M == 0 || N == 0 || K == 0 || !use_split(M, N, K, bits, group_size, x_dtype, sb_dtype))
     return jq_quantized_matmul(x, x_dtype, codes, scales, biases, sb_dtype, bits, group_size, M,
                                N, K, y, y_dtype, stream);

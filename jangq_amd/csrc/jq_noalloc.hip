@@ -8,7 +8,8 @@
 // passed to kernels (the array's name in host code is a host-side stand-in, not a device
 // address). Every call on one GPU shares the array: calls that overlap on a GPU race, and the
 // array keeps the last call's contents. The K-split kernel writes every partial it later reads
-// within the same call, so nothing needs clearing between calls.
+// within the same call, and the prefill GEMM every f16 activation row and exponent it reads,
+// so nothing needs clearing between calls.
 #include <mutex>
 
 #include "jq_common.h"
@@ -52,7 +53,9 @@ int jq_quantized_matmul_noalloc(const void* x, int x_dtype, const uint32_t* code
   if (need <= 0)  // no scratch used (or invalid sizes, which the matmul reports)
     return jq_quantized_matmul(x, x_dtype, codes, scales, biases, sb_dtype, bits, group_size, M,
                                N, K, y, y_dtype, stream);
-  if (need > (int64_t)JQ_NOALLOC_SCRATCH_BYTES) return JQ_ERR_WORKSPACE;
+  // The workspace form checks the array's size before any launch: the K-split decode needs
+  // its whole workspace (JQ_ERR_WORKSPACE otherwise), the prefill GEMM runs its activation
+  // rows in passes of whole 256-row tiles that fit.
   void* ws = nullptr;
   const int s = scratch_ptr(&ws);
   if (s) return s;

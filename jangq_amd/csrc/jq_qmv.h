@@ -150,6 +150,14 @@ int dmx_gather_launch(const QmmProblem& p, const QmmProblem* p2, const GatherPla
 int qmm_launch(const QmmProblem& p, int bits, int gs, int xd, int sb, int yd, hipStream_t st);
 int gemm_launch(const QmmProblem& p, int bits, int gs, int xd, int sb, int yd, hipStream_t st);
 
+// Prefill GEMM on the f16 matrix cores (jq_gemm16.hip): gs 64/128, bf16/f16 activations, every
+// width. Its workspace holds the f16 activation rows of a pass; a smaller one (at least 256
+// rows' worth) runs the rows in passes.
+bool gemm16_ok(int64_t M, int64_t K, int bits, int gs, int xd, int sb);
+int64_t gemm16_workspace(int64_t rows, int64_t N, int64_t K, int gs);
+int gemm16_launch(const QmmProblem& p, int bits, int gs, int xd, int sb, int yd, void* ws,
+                  int64_t ws_bytes, hipStream_t st);
+
 // Grouped matrix-core GEMM over expert segments described by `plan` (device data). With
 // p2 != NULL, p is the gate and p2 the up projection (same shapes) and the output is
 // silu(gate) * up (the SwitchGLU activation).

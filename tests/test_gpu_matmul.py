@@ -40,7 +40,7 @@ def run_case(M, N, K, bits, gs, xdt="bf16", sidecar="bf16", seed=0, ydt=None):
     if ydt == "f32":
         gemm = M >= GEMM_MIN_ROWS and gs in (64, 128)
         return assert_close(values_of(y), ref, f"M{M} N{N} K{K} b{bits} g{gs}",
-                            rel=1e-4 if gemm else 2e-6, mabs=2e-3 if gemm else 1e-4)
+                            rel=5e-4 if gemm else 2e-6, mabs=2e-3 if gemm else 1e-4)
     return assert_close(values_of(y), O.round_to(ref, ydt), f"M{M} N{N} K{K} b{bits} g{gs} {xdt}",
                         exact=ref, out_dtype=ydt)
 

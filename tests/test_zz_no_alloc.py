@@ -75,3 +75,26 @@ def test_noalloc_other_shapes_and_limit():
                                          sc.data_ptr(), 1, 2, 64, M, N, K, yb.data_ptr(), 1,
                                          torch.cuda.current_stream().cuda_stream)
     assert st == -7
+
+
+def test_noalloc_prefill_runs_in_passes():
+    """A prefill shape whose f16 activation rows exceed the array: the entry point runs them in
+    passes of whole 256-row tiles, bit-equal to the workspace form with a full workspace, on
+    two calls in a row (the second smaller)."""
+    lib = _lib.lib()
+    N, K, bits, gs = 1024, 4096, 4, 64
+    qw = QWeight(N, K, bits, gs, seed=81)
+    rng = np.random.default_rng(82)
+    for M in (2304, 1100):
+        x = O.round_bf16(rng.standard_normal((M, K), dtype=np.float32))
+        tx = to_tensor(x, "bf16")
+        ref, nws = _call_ws(lib, tx, qw, M, N, K, bits, gs)
+        if M == 2304:
+            assert nws > LIMIT  # the array holds fewer rows than the call has
+        st, y = _call_static(lib, tx, qw, M, N, K, bits, gs)
+        assert st == 0
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"M={M}"
+        exact = O.quantized_matmul(x[-3:], qw.packed, qw.s, qw.b, bits, gs)
+        assert_close(values_of(y)[-3:], O.round_bf16(exact), f"noalloc prefill M{M}",
+                     exact=exact, out_dtype="bf16")
