@@ -109,7 +109,13 @@ def _check_block(blk, qs, T, E, H, k, seed, skew, sample):
     rid, rw = jq.moe_route(tl, k, True)
     two = jq.switch_glu_combine(tx, rid, rw, m.gate_proj.as_tuple(), m.up_proj.as_tuple(),
                                 m.down_proj.as_tuple(), m.group_size(), None)
-    assert torch.equal(out.view(torch.int16), two.view(torch.int16)), "moe_experts != route + combine"
+    if not torch.equal(out.view(torch.int16), two.view(torch.int16)):
+        bad = (out.view(torch.int16) != two.view(torch.int16)).nonzero().tolist()
+        d = (out.float() - two.float()).abs().max().item()
+        raise AssertionError(f"moe_experts != route + combine at {len(bad)} outputs (first "
+                             f"{bad[:4]}), max |diff| {d}; ids equal "
+                             f"{torch.equal(gid, rid)}, weights bit-equal "
+                             f"{torch.equal(gw.view(torch.int32), rw.view(torch.int32))}")
     for t in sample:
         sh = None
         if "sg" in qs:
