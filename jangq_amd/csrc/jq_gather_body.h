@@ -6,6 +6,8 @@
 #include "jq_qmv.h"
 #include "jq_route.h"
 
+#include <type_traits>
+
 namespace {
 
 using namespace jq;
@@ -152,7 +154,17 @@ JQ_DEV void gather_body(const GatherArgs& a, int bid, int nblk) {
   const int ntiles = a.plan.n_tiles ? *a.plan.n_tiles
                                      : (a.plan.direct_pairs + a.plan.direct_rows - 1) / a.plan.direct_rows;
   int first, end;
-  {
+  if constexpr (ROUTE) {
+    // Routed form: nblk is a multiple of the token count (the launchers see to it) and a
+    // block's items belong to one token, so each wave routes once, before its first item.
+    const int T = ntiles / a.rk, bpt = nblk / T, tok = bid / bpt, sub = bid - tok * bpt;
+    const int items_t = a.rk * a.nrb;
+    const int per = (items_t + bpt - 1) / bpt;
+    first = tok * items_t + sub * per;
+    const int tend = (tok + 1) * items_t;
+    end = tok < T && first + per < tend ? first + per : tend;
+    if (tok >= T) end = first;
+  } else {
     const int items = (COMB ? a.ctok : ntiles) * a.nrb;
     const int per = (items + nblk - 1) / nblk;
     first = bid * per;
@@ -238,18 +250,16 @@ JQ_DEV void gather_body(const GatherArgs& a, int bid, int nblk) {
     tile = it / a.nrb;
     rbi = it - tile * a.nrb;
   }
-  // Routed form: lane j holds expert j (and its weight) of token rt_tok.
-  int rt_tok = -1;
+  // Routed form: lane j holds expert j (and its weight) of the block's token.
   uint32_t rt_id = 0;
   float rt_w = 0.f;
-  auto tile_of = [&](int t) -> int4 {
+  auto tile_of = [&](int t, auto can_route) -> int4 {
     if constexpr (ROUTE) {
       const int tok = t / a.rk, j = t - tok * a.rk;
-      if (tok != rt_tok) {  // wave-uniform
+      if constexpr (decltype(can_route)::value) {  // the wave's first item only
         jqr::route_wave<kRouteSlots>(
             (const char*)a.rlogits + (int64_t)tok * a.rE * (a.ro.logit_dtype == JQ_F32 ? 4 : 2),
             a.rE, a.rk, a.ro, lane, rt_id, rt_w);
-        rt_tok = tok;
       }
       const uint32_t e = (uint32_t)__builtin_amdgcn_readlane((int)rt_id, j);
       const bool ok = e < (uint32_t)a.plan.E;
@@ -268,7 +278,7 @@ JQ_DEV void gather_body(const GatherArgs& a, int bid, int nblk) {
       }
     }
   };
-  int4 tl = tile_of(tile);
+  int4 tl = tile_of(tile, std::true_type{});
   publish(tile, rbi);
   TileRows<MT> tr;
   tile_rows<MT>(a.plan, tl, tr);
@@ -291,7 +301,7 @@ JQ_DEV void gather_body(const GatherArgs& a, int bid, int nblk) {
     const int tile2 = more && wrap ? tile + (COMB ? a.ck : 1) : tile;
     const int rbi2 = more ? (wrap ? 0 : rbi + 1) : rbi;
     const int ct2 = more && wrap ? ct + 1 : ct;
-    const int4 tl2 = tile_of(tile2);
+    const int4 tl2 = tile_of(tile2, std::false_type{});
     if (more) publish(tile2, rbi2);
     const int64_t row02 = (int64_t)rbi2 * ROWS;
     Rsrc rc2[NB], rs2[NB], rb2[NB];

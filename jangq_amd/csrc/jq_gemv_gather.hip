@@ -63,8 +63,13 @@ int launch_g(GatherArgs& a, int64_t max_tiles, hipStream_t st) {
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
   const int64_t cap = (int64_t)nb * cus;
-  const int grid = (int)(units < cap ? units : cap);
-  gemv_gather_kernel<D, SB, MT, RBL, NB, RW, COMB, ROUTE><<<grid, 64 * kw, 0, st>>>(a);
+  int64_t grid = units < cap ? units : cap;
+  if constexpr (ROUTE) {  // whole tokens per block range: a multiple of the token count
+    const int64_t T = max_tiles / a.rk;
+    grid = (grid / T > 0 ? grid / T : 1) * T;
+    if (grid >= ((int64_t)1 << 31)) return JQ_ERR_SHAPE;
+  }
+  gemv_gather_kernel<D, SB, MT, RBL, NB, RW, COMB, ROUTE><<<(unsigned)grid, 64 * kw, 0, st>>>(a);
   return jqh::launch_status();
 }
 

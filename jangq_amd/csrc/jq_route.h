@@ -73,6 +73,16 @@ JQ_DEV float wave_max_f32(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// A pointer that every lane holds, moved to scalar registers so that buffer descriptors built
+// from it are wave-uniform.
+template <class T>
+JQ_DEV const T* uniform_ptr(const T* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const T*)(((uint64_t)hi << 32) | lo);
+}
+
 JQ_DEV float lane_read(float v, int l) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
@@ -92,21 +102,39 @@ JQ_DEV float gate_score(int score, float v) {
 template <int SL>
 JQ_DEV void route_wave(const void* __restrict__ row, int E, int k, const RouteOpts& o, int lane,
                        uint32_t& id, float& w) {
+  // All SL logits (and biases) of a lane are requested before any is used: range-checked
+  // buffer loads (slots past E read 0 and touch no memory) under a wave-uniform dtype branch,
+  // so the loads stay in flight together instead of one round trip each.
   float v[SL];
+  float bias[SL];
+  {
+    const bool f32 = o.logit_dtype == JQ_F32;
+    const jqg::Rsrc rl = jqg::make_rsrc(uniform_ptr(row), (uint32_t)E * (f32 ? 4u : 2u));
+    uint32_t raw[SL];
+    if (f32) {
+#pragma unroll
+      for (int i = 0; i < SL; ++i)
+        raw[i] = __builtin_amdgcn_raw_buffer_load_b32(rl, (uint32_t)(lane + 64 * i) * 4u, 0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < SL; ++i)
+        raw[i] = __builtin_amdgcn_raw_buffer_load_b16(rl, (uint32_t)(lane + 64 * i) * 2u, 0, 0);
+    }
+    const jqg::Rsrc rbias = jqg::make_rsrc(uniform_ptr(o.bias), o.bias ? (uint32_t)E * 4u : 0u);
+#pragma unroll
+    for (int i = 0; i < SL; ++i)
+      bias[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rbias, (uint32_t)(lane + 64 * i) * 4u, 0, 0));
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+      const float x = f32 ? __uint_as_float(raw[i])
+                      : o.logit_dtype == JQ_BF16 ? __uint_as_float(raw[i] << 16)
+                                                 : jq::f16_bits_to_f32((uint16_t)raw[i]);
+      v[i] = lane + 64 * i < E ? x + 0.0f : -INFINITY;  // -0 becomes +0
+    }
+  }
   float mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < SL; ++i) {
-    const int e = lane + 64 * i;
-    float x = -INFINITY;
-    if (e < E) {
-      x = o.logit_dtype == JQ_BF16 ? jq::load_t<JQ_BF16>(row, e)
-          : o.logit_dtype == JQ_F16 ? jq::load_t<JQ_F16>(row, e)
-                                    : ((const float*)row)[e];
-      x += 0.0f;  // -0 becomes +0
-    }
-    v[i] = x;
-    mx = fmaxf(mx, v[i]);
-  }
+  for (int i = 0; i < SL; ++i) mx = fmaxf(mx, v[i]);
   const bool soft = o.score == kSoftmax;
   float inv = 1.f;
   if (soft) {
@@ -127,7 +155,7 @@ JQ_DEV void route_wave(const void* __restrict__ row, int E, int k, const RouteOp
   for (int i = 0; i < SL; ++i) {
     const int e = lane + 64 * i;
     float sel = v[i];
-    if (!by_logit) sel = score_of(v[i]) + (o.bias && e < E ? o.bias[e] : 0.f) + 0.0f;
+    if (!by_logit) sel = score_of(v[i]) + bias[i] + 0.0f;  // (0 without a bias or past E)
     key[i] = e < E ? ord_key(sel) : 0u;
   }
   if (grouped) {
