@@ -257,9 +257,13 @@ JQ_DEV void gather_body(const GatherArgs& a, int bid, int nblk) {
     if constexpr (ROUTE) {
       const int tok = t / a.rk, j = t - tok * a.rk;
       if constexpr (decltype(can_route)::value) {  // the wave's first item only
+        // Rounds up to the last slot the wave's items use; all k for the wave that publishes
+        // the token's ids and weights, and for renormalised weights that enter h.
+        const int last = (end - 1) / a.nrb - tok * a.rk;
+        const bool all = first == tok * a.rk * a.nrb || (a.rbefore && a.ro.renorm);
         jqr::route_wave<kRouteSlots>(
             (const char*)a.rlogits + (int64_t)tok * a.rE * (a.ro.logit_dtype == JQ_F32 ? 4 : 2),
-            a.rE, a.rk, a.ro, lane, rt_id, rt_w);
+            a.rE, a.rk, a.ro, lane, rt_id, rt_w, all ? a.rk : last + 1);
       }
       const uint32_t e = (uint32_t)__builtin_amdgcn_readlane((int)rt_id, j);
       const bool ok = e < (uint32_t)a.plan.E;

@@ -101,7 +101,7 @@ JQ_DEV float gate_score(int score, float v) {
 // row: the token's E logits of o.logit_dtype (converted exactly to fp32).
 template <int SL>
 JQ_DEV void route_wave(const void* __restrict__ row, int E, int k, const RouteOpts& o, int lane,
-                       uint32_t& id, float& w) {
+                       uint32_t& id, float& w, int rounds = 64) {
   // All SL logits (and biases) of a lane are requested before any is used: range-checked
   // buffer loads (slots past E read 0 and touch no memory) under a wave-uniform dtype branch,
   // so the loads stay in flight together instead of one round trip each.
@@ -195,7 +195,10 @@ JQ_DEV void route_wave(const void* __restrict__ row, int E, int k, const RouteOp
 
   uint64_t mine = 0;  // lane j: round j's (key, ~id)
   float sc = 0.f;     // lane j: round j's score
-  for (int j = 0; j < k; ++j) {
+  // Only the first `rounds` experts when the caller needs no more (their ids and unrenormalised
+  // weights are final after their own rounds; renormalised weights need all k).
+  const int nr = rounds < k ? rounds : k;
+  for (int j = 0; j < nr; ++j) {
     // The lane's largest remaining key; a strict > in slot order keeps the lowest id.
     uint32_t bk = 0;
     int bi = 0;
