@@ -212,11 +212,7 @@ JQ_DEV void gather_body(const GatherArgs& a, int bid, int nblk) {
                       RowSlot<NW, UPL>& slot) {
     const int q = r % NB, rr = (sr * RBL + r) / NB;
     load_chunk<NW>(rc[q], voff + rr * rowbytes, slot.w);
-#pragma unroll
-    for (int t = 0; t < UPL; ++t) {
-      slot.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs[q], vsb[t] + rr * sbrow, 0, 0);
-      slot.b[t] = __builtin_amdgcn_raw_buffer_load_b16(rb[q], vsb[t] + rr * sbrow, 0, 0);
-    }
+    load_sb<D>(rs[q], rb[q], vsb, rr * sbrow, slot);
   };
   XState xs[UPL][MT];
   auto load_x = [&](const TileRows<MT>& tr) {

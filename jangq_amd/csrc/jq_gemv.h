@@ -155,4 +155,24 @@ struct RowSlot {
   uint32_t s[UPL], b[UPL];
 };
 
+// Scale and bias words of a lane chunk's UPL units, at byte offsets vsb[t] + off of the
+// sidecar rows. The two units of a 2-bit chunk lie in one group when groups hold at least 64
+// codes (D::GS >= 64; 32-code groups are instantiated with GS = 32): one load each then
+// serves both units.
+template <class D, int NW, int UPL>
+JQ_DEV void load_sb(Rsrc rs, Rsrc rb, const uint32_t* vsb, uint32_t off, RowSlot<NW, UPL>& slot) {
+  if constexpr (UPL == 2 && D::GS >= 64) {
+    const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b16(rs, vsb[0] + off, 0, 0);
+    const uint32_t bv = __builtin_amdgcn_raw_buffer_load_b16(rb, vsb[0] + off, 0, 0);
+    slot.s[0] = slot.s[1] = sv;
+    slot.b[0] = slot.b[1] = bv;
+  } else {
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) {
+      slot.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs, vsb[t] + off, 0, 0);
+      slot.b[t] = __builtin_amdgcn_raw_buffer_load_b16(rb, vsb[t] + off, 0, 0);
+    }
+  }
+}
+
 }  // namespace jqg

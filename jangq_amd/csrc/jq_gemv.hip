@@ -99,11 +99,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_kernel(GemvArgs a) {
   };
   auto load_row = [&](Rsrc rc, Rsrc rs, Rsrc rb, int r, RowSlot<NW, UPL>& slot) {
     load_chunk<NW>(rc, voff + r * rowbytes, slot.w);
-#pragma unroll
-    for (int t = 0; t < UPL; ++t) {
-      slot.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs, vsb[t] + r * sbrow, 0, 0);
-      slot.b[t] = __builtin_amdgcn_raw_buffer_load_b16(rb, vsb[t] + r * sbrow, 0, 0);
-    }
+    load_sb<D>(rs, rb, vsb, r * sbrow, slot);
   };
 
   int p;
@@ -301,18 +297,30 @@ int launch_glu(GemvArgs& a, hipStream_t st) {
   return launch_row<D, SB, 2, 2, true>(a, st);
 }
 
-template <int BITS, int XDT>
-int launch_glu_sb(GemvArgs& a, int sb, hipStream_t st) {
-  using D = Dc<BITS, 64, XDT>;
+// The group size is a run-time argument of these kernels; D::GS is 32 only for 2-bit codes in
+// 32-code groups (a lane chunk's two units then hold two groups), 64 otherwise.
+template <class D>
+int launch_glu_d(GemvArgs& a, int sb, hipStream_t st) {
   if (sb == JQ_BF16) return launch_glu<D, JQ_BF16>(a, st);
   return launch_glu<D, JQ_F16>(a, st);
 }
-
 template <int BITS, int XDT>
-int launch_sb(GemvArgs& a, int sb, hipStream_t st) {
-  using D = Dc<BITS, 64, XDT>;  // the group size is a run-time argument of this kernel
+int launch_glu_sb(GemvArgs& a, int sb, hipStream_t st) {
+  if constexpr (BITS == 2)
+    if (a.ushift == 0) return launch_glu_d<Dc<2, 32, XDT>>(a, sb, st);
+  return launch_glu_d<Dc<BITS, 64, XDT>>(a, sb, st);
+}
+
+template <class D>
+int launch_d(GemvArgs& a, int sb, hipStream_t st) {
   if (sb == JQ_BF16) return launch_m<D, JQ_BF16>(a, st);
   return launch_m<D, JQ_F16>(a, st);
+}
+template <int BITS, int XDT>
+int launch_sb(GemvArgs& a, int sb, hipStream_t st) {
+  if constexpr (BITS == 2)
+    if (a.ushift == 0) return launch_d<Dc<2, 32, XDT>>(a, sb, st);
+  return launch_d<Dc<BITS, 64, XDT>>(a, sb, st);
 }
 
 template <int BITS>

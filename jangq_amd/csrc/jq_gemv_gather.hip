@@ -102,11 +102,18 @@ int launch_mt(GatherArgs& a, int mt, int64_t max_tiles, hipStream_t st) {
   return launch_rw<D, SB, NB, 1>(a, mt, max_tiles, st);
 }
 
-template <int BITS, int XDT, int NB>
-int launch_sb(GatherArgs& a, int sb, int mt, int64_t max_tiles, hipStream_t st) {
-  using D = Dc<BITS, 64, XDT>;  // the group size is a run-time argument of this kernel
+// The group size is a run-time argument of this kernel; D::GS is 32 only for 2-bit codes in
+// 32-code groups (a lane chunk's two units then hold two groups), 64 otherwise.
+template <class D, int NB>
+int launch_d(GatherArgs& a, int sb, int mt, int64_t max_tiles, hipStream_t st) {
   if (sb == JQ_BF16) return launch_mt<D, JQ_BF16, NB>(a, mt, max_tiles, st);
   return launch_mt<D, JQ_F16, NB>(a, mt, max_tiles, st);
+}
+template <int BITS, int XDT, int NB>
+int launch_sb(GatherArgs& a, int sb, int mt, int64_t max_tiles, hipStream_t st) {
+  if constexpr (BITS == 2)
+    if (a.ushift == 0) return launch_d<Dc<2, 32, XDT>, NB>(a, sb, mt, max_tiles, st);
+  return launch_d<Dc<BITS, 64, XDT>, NB>(a, sb, mt, max_tiles, st);
 }
 
 template <int BITS, int NB>

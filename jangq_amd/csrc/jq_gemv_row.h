@@ -117,11 +117,7 @@ JQ_DEV void gemv_row_body(const GemvArgs& a, int it, int nwaves, const Fin& fin)
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       load_chunk<NW>(rc, voff[j] + r * rowbytes, slot[j].w);
-#pragma unroll
-      for (int t = 0; t < UPL; ++t) {
-        slot[j].s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs, vsb[j][t] + r * sbrow, 0, 0);
-        slot[j].b[t] = __builtin_amdgcn_raw_buffer_load_b16(rb, vsb[j][t] + r * sbrow, 0, 0);
-      }
+      load_sb<D>(rs, rb, vsb[j], r * sbrow, slot[j]);
     }
   };
   int p;

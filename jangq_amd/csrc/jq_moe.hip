@@ -726,6 +726,7 @@ bool fused_ok(const MoeRun& r) {
   if (r.sg->sb_dtype != JQ_BF16 || r.su->sb_dtype != JQ_BF16) return false;
   auto lowbits = [](int b) { return b >= 2 && b <= 4; };
   if (!lowbits(r.bits_gu) || (r.sg->bits != 4 && r.sg->bits != 8)) return false;
+  if (r.bits_gu == 2 && r.gs < 64) return false;  // (the fused launch has GS = 64 forms only)
   if (!jqk::gemv_gather_route_ok(r.E, r.k)) return false;
   if (!jqk::gemv_gather_ok(r.I, r.H, r.bits_gu, r.gs, r.xd, r.sb) ||
       jqk::fused_rw(r.H, r.bits_gu) > 2)
