@@ -283,6 +283,37 @@ JQ_DEV void gather_body(const GatherArgs& a, int bid, int nblk) {
   TileRows<MT> tr;
   tile_rows<MT>(a.plan, tl, tr);
   int64_t row0 = (int64_t)rbi * ROWS;
+  // Combined form: the combine's routing weights, shared row and shared-gate logit of an item
+  // are requested together with the item's rows, so they sit in registers by the combine
+  // instead of costing a dependent round trip at its end. Range-checked buffer loads without
+  // a branch (lanes past the slots or rows read 0 or a value that is not used); 16-bit
+  // halves, so every output dtype takes the same two loads.
+  uint32_t pw = 0, psh = 0, psh_hi = 0, pgl = 0, pgl_hi = 0;
+  auto prefetch = [&](int ctk, int64_t r0) {
+    if constexpr (COMB) {
+      const uint32_t es = a.yd == JQ_F32 ? 4u : 2u;
+      const Rsrc rw = make_rsrc(a.cw ? a.cw + (int64_t)ctk * a.ck : nullptr,
+                                a.cw && !a.cbefore ? (uint32_t)a.ck * 4u : 0u);
+      pw = __builtin_amdgcn_raw_buffer_load_b32(rw, (uint32_t)lane * 4u, 0, 0);
+      const int64_t nr = N - r0 < ROWS ? N - r0 : ROWS;
+      const Rsrc rsh = make_rsrc(a.cshared ? (const char*)a.cshared + ((int64_t)ctk * N + r0) * es
+                                           : nullptr,
+                                 a.cshared ? (uint32_t)nr * es : 0u);
+      psh = __builtin_amdgcn_raw_buffer_load_b16(rsh, (uint32_t)lane * es, 0, 0);
+      psh_hi = __builtin_amdgcn_raw_buffer_load_b16(rsh, (uint32_t)lane * es + 2u, 0, 0);
+      const Rsrc rg = make_rsrc(a.cgate ? (const char*)a.cgate + (int64_t)ctk * es : nullptr,
+                                a.cgate ? es : 0u);
+      pgl = __builtin_amdgcn_raw_buffer_load_b16(rg, 0u, 0, 0);
+      pgl_hi = __builtin_amdgcn_raw_buffer_load_b16(rg, 2u, 0, 0);
+    }
+  };
+  // (the halves are joined only where the value is used, so the loads need not have landed
+  // when they are issued)
+  auto out_value = [&](uint32_t lo, uint32_t hi) {
+    return a.yd == JQ_F32 ? __uint_as_float((lo & 0xFFFFu) | (hi << 16))
+           : a.yd == JQ_BF16 ? __uint_as_float(lo << 16) : f16_bits_to_f32((uint16_t)lo);
+  };
+  prefetch(ct, row0);
   Rsrc rc[NB], rs[NB], rbv[NB];
   views(tl, row0, true, rc, rs, rbv);
   RowSlot<NW, UPL> ring[RBL];
@@ -346,10 +377,9 @@ JQ_DEV void gather_body(const GatherArgs& a, int bid, int nblk) {
         float comb = 0.f;
         for (int j = 0; j < a.ck; ++j) {
           const float y = round_out(red[par][j][lane], a.yd);
-          comb = a.cbefore ? comb + y : fmaf(a.cw[ct * a.ck + j], y, comb);
+          comb = a.cbefore ? comb + y : fmaf(jqr::lane_read(__uint_as_float(pw), j), y, comb);
         }
-        const float sh = a.cshared ? load_out(a.cshared, (int64_t)ct * N + row, a.yd) : 0.f;
-        const float gl = a.cgate ? load_out(a.cgate, ct, a.yd) : 0.f;
+        const float sh = out_value(psh, psh_hi), gl = out_value(pgl, pgl_hi);
         store_out(a.cout, (int64_t)ct * N + row,
                   jqk::moe_final(a.cbefore, comb, a.cshared != nullptr, sh, a.cgate != nullptr, gl,
                                  a.yd),
@@ -386,6 +416,11 @@ JQ_DEV void gather_body(const GatherArgs& a, int bid, int nblk) {
       // New tile: its activation rows replace the registers (the ring keeps the next rows).
       tile_rows<MT>(a.plan, tl2, tr);
       load_x(tr);
+    }
+    if constexpr (COMB) {
+      // the next item's combine inputs, once this item's are consumed (after its combine)
+      __builtin_amdgcn_sched_barrier(0);
+      prefetch(ct2, row02);
     }
     it += 1;
     tile = tile2;
