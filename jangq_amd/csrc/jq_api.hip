@@ -44,12 +44,22 @@ jqk::QmmProblem dense_problem(const void* x, const uint32_t* codes, const void* 
   return p;
 }
 
+// The vector-ALU GEMV serves up to 4 activation rows (2 at 2 bits); from 3 rows, outputs of
+// more than kGemvRowsMax rows run faster on the matrix-core kernel. Measured on MI355X (graph,
+// rotated weights): gate|up 2 x 14336 x 4096 3-bit at 3 / 4 rows 25.9 / 26.5 -> 18.1 /
+// 18.6 us; 4096-row outputs within 5% either way (o 6-bit 8.8 against 9.2 us: kept).
+constexpr int64_t kGemvRowsMax = 8192;
+bool prefer_gemv(int M, int64_t K, int64_t maxN, int bits, int gs, int xd, int sb) {
+  if (!jqk::gemv_ok(M, K, maxN, bits, gs, xd, sb)) return false;
+  return M <= 2 || maxN <= kGemvRowsMax || !jqk::dmx_ok(M, K, maxN, bits, gs, xd, sb, 1);
+}
+
 int dense_one(const void* x, int xd, const uint32_t* codes, const void* scales,
               const void* biases, int sb, int bits, int gs, int64_t M, int64_t N, int64_t K,
               void* y, int yd, hipStream_t st) {
   const bool mfma_ok = (xd == JQ_BF16 || xd == JQ_F16) && K % 128 == 0;
   const int Mi = (int)(M < (1 << 30) ? M : (1 << 30));
-  if (jqk::gemv_ok(Mi, K, N, bits, gs, xd, sb)) {
+  if (prefer_gemv(Mi, K, N, bits, gs, xd, sb)) {
     jqk::QmvBatch b;
     b.M = Mi;
     b.K = (int)K;
@@ -231,7 +241,7 @@ int jq_quantized_matmul_multi(int count, const void* const* x, int x_dtype,
   const int M0 = (int)(M[0] < (1 << 30) ? M[0] : (1 << 30));
   int64_t maxN = 0;
   for (int i = 0; i < count; ++i) maxN = N[i] > maxN ? N[i] : maxN;
-  const bool gemv = same && jqk::gemv_ok(M0, K[0], maxN, bits[0], group_size[0], x_dtype, sb_dtype);
+  const bool gemv = same && prefer_gemv(M0, K[0], maxN, bits[0], group_size[0], x_dtype, sb_dtype);
   const bool q4 = same && !gemv && use_qmv4(M[0], K[0]) &&
                   jqk::qmv4_ok(M0, K[0], maxN, bits[0], group_size[0], x_dtype, sb_dtype);
   const bool dmx = same && !gemv && !q4 && M[0] <= kDecpMaxRows &&

@@ -113,6 +113,14 @@ def test_c2_projection_shapes(N, K, bits):
     run_case(8, N, K, bits, 64, seed=N + bits + 1)
 
 
+@pytest.mark.parametrize("M", [3, 4])
+@pytest.mark.parametrize("N,bits,gs", [(14336, 3, 64), (9000, 4, 128), (4096, 6, 64)])
+def test_small_batches_long_outputs(M, N, bits, gs):
+    """3-4 activation rows: outputs of more than 8192 rows take the matrix-core kernel, shorter
+    ones the vector GEMV; both against the oracle."""
+    run_case(M, N, 4096, bits, gs, seed=M * 31 + N + bits)
+
+
 @pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 def test_long_row_decode_batches(bits, gs):
