@@ -75,7 +75,10 @@ int moe_fused_gu_launch(const QmmProblem& g, const QmmProblem& u, const GatherPl
   ga.nrb = (int)((I + rows - 1) / rows);
   row_args(a.s, sg, &su, (int)H, gs_s, JQ_BF16, limit, 2, true);
   const int64_t itemsA = (int64_t)k * ga.nrb;
-  const double bytesA = 2.0 * k * I * (H * bits_r / 8 + H / gs_r * 4);
+  // The routed half's bytes weigh 1.5x in the grid split: its waves first run the top-k and
+  // look up their experts. Measured at config 5 (T = 1): weights 1.0 / 1.2 / 1.4-1.6 / 1.8 of
+  // the bytes gave the layer 44.1 / 42.9 / 42.3 / 44.8 us.
+  const double bytesA = 1.5 * 2.0 * k * I * (H * bits_r / 8 + H / gs_r * 4);
   const double bytesB = 2.0 * Is * (H * bits_s / 8 + H / gs_s * 4);
 #define JQ_R(BR, RW)                                                                          \
   if (bits_r == BR && rw == RW)                                                               \
