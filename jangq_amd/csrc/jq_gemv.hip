@@ -191,9 +191,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) gemv_kernel(GemvArgs a) {
   }
 }
 
-template <class D, int SB, int CPL, int RB, bool GLU = false>
+template <class D, int SB, int CPL, int RB, bool GLU = false, bool SHARE = false>
 __global__ void __launch_bounds__(256) gemv_row_kernel(GemvArgs a) {
-  gemv_row_body<D, SB, CPL, RB, GLU>(
+  static_assert(CPL * 64 * row_upl<D::BITS>() <= 256, "one unit of x per thread");
+  gemv_row_body<D, SB, CPL, RB, GLU, RowStore, SHARE>(
       a, __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)),
       (int)gridDim.x * 4, RowStore());
 }
@@ -214,18 +215,30 @@ int launch_row(GemvArgs& a, hipStream_t st) {
     for (int i = a.nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
   }
   if (total == 0) return JQ_OK;
-  int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_row_kernel<D, SB, CPL, RB, GLU>, 256, 0) !=
-          hipSuccess || nb < 1)
-    nb = 1;
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
-  const int64_t cap = (int64_t)nb * cus * 4;  // waves
-  const int64_t iters = (total + cap - 1) / cap;
-  const int64_t waves = (total + iters - 1) / iters;
-  gemv_row_kernel<D, SB, CPL, RB, GLU><<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(a);
+  // Waves (all resident at once) and items per wave for one form of the kernel.
+  auto shape = [&](auto kern, int64_t& waves, int64_t& iters) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 256, 0) != hipSuccess || nb < 1)
+      nb = 1;
+    const int64_t cap = (int64_t)nb * cus * 4;
+    iters = (total + cap - 1) / cap;
+    waves = (total + iters - 1) / iters;
+  };
+  // Waves with several items build the activation state once per block (measured at config 2:
+  // gate|up, 3 items per wave, 13.0 -> 12.6 us); with one item per wave the barrier is only
+  // latency (q|k|v, o and config 1 each 0.1-0.2 us slower), so every wave builds its own.
+  int64_t waves = 0, iters = 0;
+  shape(gemv_row_kernel<D, SB, CPL, RB, GLU, false>, waves, iters);
+  if (iters >= 2) {
+    shape(gemv_row_kernel<D, SB, CPL, RB, GLU, true>, waves, iters);
+    gemv_row_kernel<D, SB, CPL, RB, GLU, true><<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(a);
+  } else {
+    gemv_row_kernel<D, SB, CPL, RB, GLU, false><<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(a);
+  }
   return jqh::launch_status();
 }
 
@@ -277,11 +290,12 @@ int launch_m(GemvArgs& a, hipStream_t st) {
     if (kw >= 4) return launch_rb<D, SB, 1, 16>(a, st);
     int64_t rows = 0;
     for (int i = 0; i < a.nprob; ++i) rows += a.b.p[i].N;
+    const int cpl = row_cpl(a.b.K, D::BITS);
     if (rows <= kFewRows) {  // short outputs (routers): one row per item, twice the waves
-      if (kw == 1) return launch_row<D, SB, 1, 1>(a, st);
+      if (cpl == 1) return launch_row<D, SB, 1, 1>(a, st);
       return launch_row<D, SB, 2, 1>(a, st);
     }
-    if (kw == 1) return launch_row<D, SB, 1, 2>(a, st);
+    if (cpl == 1) return launch_row<D, SB, 1, 2>(a, st);
     return launch_row<D, SB, 2, 2>(a, st);
   }
   if (a.b.M == 2) return launch_rb<D, SB, 2, 4>(a, st);
@@ -291,14 +305,14 @@ int launch_m(GemvArgs& a, hipStream_t st) {
 
 template <class D, int SB>
 int launch_glu(GemvArgs& a, hipStream_t st) {
-  const int kw = gemv_waves(a.b.K, D::BITS, nullptr);
-  if (a.b.M != 1 || kw > 2) return JQ_ERR_SHAPE;
-  if (kw == 1) return launch_row<D, SB, 1, 2, true>(a, st);
+  const int cpl = row_cpl(a.b.K, D::BITS);
+  if (a.b.M != 1 || cpl > 2) return JQ_ERR_SHAPE;
+  if (cpl == 1) return launch_row<D, SB, 1, 2, true>(a, st);
   return launch_row<D, SB, 2, 2, true>(a, st);
 }
 
-// The group size is a run-time argument of these kernels; D::GS is 32 only for 2-bit codes in
-// 32-code groups (a lane chunk's two units then hold two groups), 64 otherwise.
+// The group size is a run-time argument of these kernels; D::GS is 32 only for codes in
+// 32-code groups whose lane chunks hold two units (two groups then), 64 otherwise.
 template <class D>
 int launch_glu_d(GemvArgs& a, int sb, hipStream_t st) {
   if (sb == JQ_BF16) return launch_glu<D, JQ_BF16>(a, st);
@@ -306,8 +320,8 @@ int launch_glu_d(GemvArgs& a, int sb, hipStream_t st) {
 }
 template <int BITS, int XDT>
 int launch_glu_sb(GemvArgs& a, int sb, hipStream_t st) {
-  if constexpr (BITS == 2)
-    if (a.ushift == 0) return launch_glu_d<Dc<2, 32, XDT>>(a, sb, st);
+  if constexpr (row_upl<BITS>() == 2)
+    if (a.ushift == 0) return launch_glu_d<Dc<BITS, 32, XDT>>(a, sb, st);
   return launch_glu_d<Dc<BITS, 64, XDT>>(a, sb, st);
 }
 
@@ -318,8 +332,8 @@ int launch_d(GemvArgs& a, int sb, hipStream_t st) {
 }
 template <int BITS, int XDT>
 int launch_sb(GemvArgs& a, int sb, hipStream_t st) {
-  if constexpr (BITS == 2)
-    if (a.ushift == 0) return launch_d<Dc<2, 32, XDT>>(a, sb, st);
+  if constexpr (BITS == 2 || row_upl<BITS>() == 2)
+    if (a.ushift == 0) return launch_d<Dc<BITS, 32, XDT>>(a, sb, st);
   return launch_d<Dc<BITS, 64, XDT>>(a, sb, st);
 }
 

@@ -51,9 +51,10 @@ int moe_fused_gu_launch(const QmmProblem& g, const QmmProblem& u, const GatherPl
   const int rw = fused_rw(H, bits_r);
   int kws = 0;
   const int kwR = rw == 1 ? jqg::gemv_waves(H, bits_r, &kws) : 1;
-  const int cpls = jqg::gemv_waves(H, bits_s, nullptr);
+  const int cpls = row_cpl(H, bits_s);
   // (2-bit routed codes in 32-code groups would need the GS = 32 instantiation)
-  if (rw > 2 || kwR > jqg::kMaxWaves || cpls > 2 || (bits_r == 2 && gs_r < 64))
+  if (rw > 2 || kwR > jqg::kMaxWaves || cpls > 2 || (bits_r == 2 && gs_r < 64) ||
+      (((JQ_ROW_UPL2 >> bits_s) & 1) && gs_s < 64))
     return JQ_ERR_SHAPE;
   FusedGuArgs a;
   GatherArgs& ga = a.g;
