@@ -3,8 +3,72 @@
 // LDS-streamed 16x16x32 kernel for K <= 4096, the register-streamed one otherwise), the
 // prefill GEMM and, for shapes none of those takes, the older LDS-tiled GEMM or the generic
 // GEMV.
+#include <mutex>
+#include <vector>
+
 #include "jq_common.h"
 #include "jq_qmv.h"
+
+namespace jqh {
+
+namespace {
+struct Occ {
+  const void* kern;
+  int threads;
+  size_t lds;
+  int dev;
+  int nb;  // resident blocks per CU; -1: dynamic LDS opt-in recorded
+};
+std::mutex g_geo_mu;
+std::vector<Occ> g_geo;
+constexpr int kMaxDevices = 64;
+int g_cus[kMaxDevices];  // 0: not queried yet
+
+int current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = 0;
+  return dev;
+}
+}  // namespace
+
+int cus() {
+  const int dev = current_device();
+  std::lock_guard<std::mutex> lk(g_geo_mu);
+  if (g_cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+      n = 256;
+    g_cus[dev] = n;
+  }
+  return g_cus[dev];
+}
+
+int blocks_per_cu(const void* kern, int threads, size_t lds) {
+  const int dev = current_device();
+  std::lock_guard<std::mutex> lk(g_geo_mu);
+  for (const Occ& o : g_geo)
+    if (o.kern == kern && o.threads == threads && o.lds == lds && o.dev == dev && o.nb > 0)
+      return o.nb;
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, threads, lds) != hipSuccess || nb < 1)
+    nb = 1;
+  g_geo.push_back(Occ{kern, threads, lds, dev, nb});
+  return nb;
+}
+
+bool set_lds(const void* kern, size_t lds) {
+  if (lds <= 64 * 1024) return true;
+  const int dev = current_device();
+  std::lock_guard<std::mutex> lk(g_geo_mu);
+  for (const Occ& o : g_geo)
+    if (o.kern == kern && o.lds == lds && o.dev == dev && o.nb == -1) return true;
+  if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return false;
+  g_geo.push_back(Occ{kern, 0, lds, dev, -1});
+  return true;
+}
+
+}  // namespace jqh
 
 namespace {
 

@@ -274,4 +274,12 @@ inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? JQ_OK : JQ_ERR_LAUNCH;
 }
+// Launch geometry on the host, each value queried from the runtime once per device (and
+// kernel, block size, LDS bytes) and then served from a cache: the queries cost microseconds
+// of host time, which is most of an eager decode launch. Defined in jq_api.hip.
+int cus();  // compute units of the current device
+int blocks_per_cu(const void* kern, int threads, size_t lds);  // resident blocks per CU, >= 1
+// Opt a kernel in to `lds` bytes of dynamic LDS on the current device (above the 64 KB
+// default); false if the runtime refuses.
+bool set_lds(const void* kern, size_t lds);
 }  // namespace jqh

@@ -322,17 +322,8 @@ int launch_cfg(DecpArgs& a, int kw, hipStream_t st) {
   const size_t lds =
       64 + (size_t)S * a.mrows * kTokStride + (size_t)2 * kw * RT * NA * TPL * 64 * 4;
   auto kern = decp_kernel<D, SB, RT, NA, SW>;
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)lds) != hipSuccess)
-    return JQ_ERR_LAUNCH;
-  int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 64 * kw, lds) != hipSuccess || nb < 1)
-    nb = 1;
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 256;
-  const int64_t cap = (int64_t)nb * cus;
+  if (!jqh::set_lds((const void*)kern, lds)) return JQ_ERR_LAUNCH;
+  const int64_t cap = (int64_t)jqh::blocks_per_cu((const void*)kern, 64 * kw, lds) * jqh::cus();
   const int64_t iters = (total + cap - 1) / cap;
   const int grid = (int)((total + iters - 1) / iters);
   kern<<<grid, 64 * kw, lds, st>>>(a);

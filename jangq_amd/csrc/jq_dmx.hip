@@ -634,17 +634,8 @@ int launch_cfg(DmxArgs& a, int kw, int64_t max_items, hipStream_t st) {
   const size_t lds = dmx_lds_bytes<D, RT, NA, SW, NSLOT>(kw);
   if (lds > (size_t)kLdsMax) return JQ_ERR_SHAPE;
   auto kern = dmx_kernel<D, SB, RT, NA, SW, NSLOT, GATHER, NB, SPLIT>;
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)lds) != hipSuccess)
-    return JQ_ERR_LAUNCH;
-  int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 64 * kw, lds) != hipSuccess || nb < 1)
-    nb = 1;
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 256;
-  int64_t cap = (int64_t)nb * cus;
+  if (!jqh::set_lds((const void*)kern, lds)) return JQ_ERR_LAUNCH;
+  int64_t cap = (int64_t)jqh::blocks_per_cu((const void*)kern, 64 * kw, lds) * jqh::cus();
   int64_t grid;
   int ny = 1;
   if constexpr (GATHER) {

@@ -365,10 +365,8 @@ __global__ void __launch_bounds__(NTH, 1) gemm_kernel(GemmArgs a) {
 
 template <class D, int SB, int SPG>
 int launch_g(const GemmArgs& a, hipStream_t st) {
-  const size_t lds = sizeof(Smem);  // above the 64 KB default: opt in (per launch, per device)
-  if (hipFuncSetAttribute((const void*)gemm_kernel<D, SB, SPG>,
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-    return JQ_ERR_LAUNCH;
+  const size_t lds = sizeof(Smem);  // above the 64 KB default: opt in (per device)
+  if (!jqh::set_lds((const void*)gemm_kernel<D, SB, SPG>, lds)) return JQ_ERR_LAUNCH;
   dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM));
   gemm_kernel<D, SB, SPG><<<grid, NTH, lds, st>>>(a);
   return jqh::launch_status();

@@ -568,8 +568,7 @@ template <int BITS, int SB>
 int launch_g16(const G16Args& a, hipStream_t st) {
   using L = G16<BITS>;
   const void* kern = (const void*)gemm16_kernel<BITS, SB>;
-  if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, L::LDS) != hipSuccess)
-    return JQ_ERR_LAUNCH;
+  if (!jqh::set_lds(kern, L::LDS)) return JQ_ERR_LAUNCH;
   dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM));
   gemm16_kernel<BITS, SB><<<grid, NTH, L::LDS, st>>>(a);
   return jqh::launch_status();

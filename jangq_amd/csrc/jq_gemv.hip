@@ -215,16 +215,9 @@ int launch_row(GemvArgs& a, hipStream_t st) {
     for (int i = a.nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
   }
   if (total == 0) return JQ_OK;
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 256;
   // Waves (all resident at once) and items per wave for one form of the kernel.
   auto shape = [&](auto kern, int64_t& waves, int64_t& iters) {
-    int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 256, 0) != hipSuccess || nb < 1)
-      nb = 1;
-    const int64_t cap = (int64_t)nb * cus * 4;
+    const int64_t cap = (int64_t)jqh::blocks_per_cu((const void*)kern, 256, 0) * jqh::cus() * 4;
     iters = (total + cap - 1) / cap;
     waves = (total + iters - 1) / iters;
   };
@@ -257,15 +250,8 @@ int launch_rb(GemvArgs& a, hipStream_t st) {
   }
   for (int i = a.nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
   if (total == 0) return JQ_OK;
-  int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_kernel<D, SB, MT, RB>, 64 * kw, 0) !=
-          hipSuccess || nb < 1)
-    nb = 1;
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 256;
-  const int64_t cap = (int64_t)nb * cus;
+  const int64_t cap =
+      (int64_t)jqh::blocks_per_cu((const void*)gemv_kernel<D, SB, MT, RB>, 64 * kw, 0) * jqh::cus();
   const int64_t iters = (total + cap - 1) / cap;
   const int grid = (int)((total + iters - 1) / iters);
   gemv_kernel<D, SB, MT, RB><<<grid, 64 * kw, 0, st>>>(a);

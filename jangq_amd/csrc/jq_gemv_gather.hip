@@ -53,16 +53,9 @@ int launch_g(GatherArgs& a, int64_t max_tiles, hipStream_t st) {
   if (max_items >= ((int64_t)1 << 31)) return JQ_ERR_SHAPE;
   a.nrb = (int)nrb;
   const int64_t units = COMB ? (int64_t)a.ctok * nrb : max_items;  // block ranges
-  int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &nb, gemv_gather_kernel<D, SB, MT, RBL, NB, RW, COMB, ROUTE>, 64 * kw, 0) != hipSuccess ||
-      nb < 1)
-    nb = 1;
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 256;
-  const int64_t cap = (int64_t)nb * cus;
+  const int64_t cap =
+      (int64_t)jqh::blocks_per_cu((const void*)gemv_gather_kernel<D, SB, MT, RBL, NB, RW, COMB, ROUTE>,
+                                  64 * kw, 0) * jqh::cus();
   int64_t grid = units < cap ? units : cap;
   if constexpr (ROUTE) {  // whole tokens per block range: a multiple of the token count
     const int64_t T = max_tiles / a.rk;

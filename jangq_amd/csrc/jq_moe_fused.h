@@ -31,14 +31,6 @@ __global__ void __launch_bounds__(64 * jqg::kMaxWaves) moe_gu_fused_kernel(Fused
   }
 }
 
-inline int cu_count() {
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 256;
-  return cus;
-}
-
 // Split `cap` resident blocks between the routed half (itemsA items, bytesA bytes) and the
 // shared half (wavesB waves of work at wpb waves per block, bytesB bytes).
 inline void split_grid(int64_t cap, int64_t itemsA, double bytesA, int64_t wavesB, int wpb,

@@ -7,12 +7,9 @@ template <class DR, int RW, class DS, int CPLS>
 int gu_launch(FusedGuArgs& a, int kwR, int64_t itemsA, double bytesA, int64_t wavesB,
               double bytesB, hipStream_t st) {
   const int threads = 64 * kwR;
-  int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, moe_gu_fused_kernel<DR, RW, DS, CPLS>,
-                                                   threads, 0) != hipSuccess ||
-      nb < 1)
-    nb = 1;
-  const int64_t cap = (int64_t)nb * cu_count();
+  const int64_t cap =
+      (int64_t)jqh::blocks_per_cu((const void*)moe_gu_fused_kernel<DR, RW, DS, CPLS>, threads, 0) *
+      jqh::cus();
   int nA = 0, nB = 0;
   split_grid(cap, itemsA, bytesA, wavesB, kwR, bytesB, nA, nB);
   a.nA = nA;

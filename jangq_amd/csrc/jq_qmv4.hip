@@ -300,14 +300,7 @@ int launch_cfg(Qmv4Args& a, int kw, hipStream_t st) {
   for (int i = a.nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
   if (total == 0) return JQ_OK;
   auto kern = qmv4_kernel<D, SB, MT, RQ, UPL>;
-  int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 64 * kw, 0) != hipSuccess || nb < 1)
-    nb = 1;
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 256;
-  const int64_t cap = (int64_t)nb * cus;
+  const int64_t cap = (int64_t)jqh::blocks_per_cu((const void*)kern, 64 * kw, 0) * jqh::cus();
   const int64_t iters = (total + cap - 1) / cap;
   const int grid = (int)((total + iters - 1) / iters);
   kern<<<grid, 64 * kw, 0, st>>>(a);

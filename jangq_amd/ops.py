@@ -32,8 +32,17 @@ def _dtype_code(t: torch.Tensor, what: str) -> int:
         raise ValueError(f"{what}: unsupported dtype {t.dtype}") from None
 
 
-def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+# The current device's current stream as a raw handle: torch's own accessor when it has one
+# (torch.cuda.current_stream() builds a Stream object and re-resolves the device, several
+# microseconds of host time per launch), else the public API.
+if hasattr(torch._C, "_cuda_getCurrentRawStream") and hasattr(torch._C, "_cuda_getDevice"):
+    _raw_stream, _cur_dev = torch._C._cuda_getCurrentRawStream, torch._C._cuda_getDevice
+
+    def _stream() -> int:
+        return _raw_stream(_cur_dev())
+else:
+    def _stream() -> int:
+        return torch.cuda.current_stream().cuda_stream
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
