@@ -138,13 +138,16 @@ JQ_DEV void load_chunk(Rsrc r, uint32_t voff, uint32_t* w) {
 constexpr int kMaxWaves = 8;
 
 // Waves per block for a K: the fewest (a power of two) for which each lane holds one chunk.
-inline int gemv_waves(int64_t K, int bits, int* shift) {
-  const int upl = bits == 2 ? 2 : 1;
+// (upl: units per lane chunk.)
+inline int gemv_waves_upl(int64_t K, int upl, int* shift) {
   const int64_t C = K / (32 * upl);
   int kw = 1, ks = 0;
   while (64 * kw < C) kw *= 2, ++ks;
   if (shift) *shift = ks;
   return kw;
+}
+inline int gemv_waves(int64_t K, int bits, int* shift) {
+  return gemv_waves_upl(K, bits == 2 ? 2 : 1, shift);
 }
 
 // One row of a lane's ring slot: the chunk's code words, and the scale and bias of each of

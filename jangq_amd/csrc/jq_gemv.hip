@@ -42,10 +42,12 @@ using jqk::QmvProblem;
 // ring of the RB rows of its current row block in registers; row r of the next row block is
 // issued right after row r of the current one has been consumed, so RB rows of loads stay in
 // flight while the block computes, reduces and stores.
-template <class D, int SB, int MT, int RB>
+// UPL_: units per lane chunk (0: units_per_chunk; 1 for long 2-bit rows, so that the row's
+// 32-code units spread over twice the waves).
+template <class D, int SB, int MT, int RB, int UPL_ = 0>
 __global__ void __launch_bounds__(64 * kMaxWaves) gemv_kernel(GemvArgs a) {
   constexpr int BITS = D::BITS;
-  constexpr int UPL = units_per_chunk<BITS>();
+  constexpr int UPL = UPL_ ? UPL_ : units_per_chunk<BITS>();
   constexpr int NW = BITS * UPL;
   __shared__ float red[2][kMaxWaves][RB * MT];
 
@@ -237,10 +239,10 @@ int launch_row(GemvArgs& a, hipStream_t st) {
 
 // Grid: as many blocks as fit the GPU at once, but no more than there are row blocks, with
 // the row blocks spread evenly (every block takes the same number, up to one).
-template <class D, int SB, int MT, int RB>
+template <class D, int SB, int MT, int RB, int UPL_ = 0>
 int launch_rb(GemvArgs& a, hipStream_t st) {
   int kws = 0;
-  const int kw = gemv_waves(a.b.K, D::BITS, &kws);
+  const int kw = UPL_ ? gemv_waves_upl(a.b.K, UPL_, &kws) : gemv_waves(a.b.K, D::BITS, &kws);
   if (kw > kMaxWaves) return JQ_ERR_SHAPE;
   a.kwshift = kws;
   int total = 0;
@@ -251,10 +253,11 @@ int launch_rb(GemvArgs& a, hipStream_t st) {
   for (int i = a.nprob; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = total;
   if (total == 0) return JQ_OK;
   const int64_t cap =
-      (int64_t)jqh::blocks_per_cu((const void*)gemv_kernel<D, SB, MT, RB>, 64 * kw, 0) * jqh::cus();
+      (int64_t)jqh::blocks_per_cu((const void*)gemv_kernel<D, SB, MT, RB, UPL_>, 64 * kw, 0) *
+      jqh::cus();
   const int64_t iters = (total + cap - 1) / cap;
   const int grid = (int)((total + iters - 1) / iters);
-  gemv_kernel<D, SB, MT, RB><<<grid, 64 * kw, 0, st>>>(a);
+  gemv_kernel<D, SB, MT, RB, UPL_><<<grid, 64 * kw, 0, st>>>(a);
   return jqh::launch_status();
 }
 
@@ -268,11 +271,22 @@ int launch_rb(GemvArgs& a, hipStream_t st) {
 // most kFewRows rows take one row per item: an 8-bit 128- or 512-expert router at K = 4096
 // 4.3 -> 3.6 us (at 4096 rows one row per item was slower, 5.2 -> 5.7 us).
 constexpr int64_t kFewRows = 1024;
+constexpr int64_t kLongFewRows = 16384;
 template <class D, int SB>
 int launch_m(GemvArgs& a, hipStream_t st) {
   constexpr bool two = D::BITS == 2;  // two units per lane chunk
   const int kw = gemv_waves(a.b.K, D::BITS, nullptr);
   if (a.b.M == 1) {
+    // Long 2-bit rows of a short output (config 2's down projection, 4096 x 14336): one
+    // 32-code unit per lane chunk, so the row spreads over twice the waves (8 per block, two
+    // per SIMD instead of one), 8 rows per block: 8.8 -> 8.0 us. With many rows the extra
+    // load instructions per byte cost more than the second wave gains (57344 rows: 61 -> 71 us).
+    if constexpr (two)
+      if (kw >= 4 && gemv_waves_upl(a.b.K, 1, nullptr) <= kMaxWaves) {
+        int64_t rows = 0;
+        for (int i = 0; i < a.nprob; ++i) rows += a.b.p[i].N;
+        if (rows <= kLongFewRows) return launch_rb<D, SB, 1, 8, 1>(a, st);
+      }
     if (kw >= 4) return launch_rb<D, SB, 1, 16>(a, st);
     int64_t rows = 0;
     for (int i = 0; i < a.nprob; ++i) rows += a.b.p[i].N;
