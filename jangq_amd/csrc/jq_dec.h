@@ -69,14 +69,20 @@ constexpr const Sched& sched() {
   else return kSched4;
 }
 
-template <int BITS_, int GS_, int XDT_>
+// F16X_ (the vector-ALU row GEMV only, 8-bit codes, bf16 activations): the activations are
+// rescaled per 32-code unit by a power of two into f16 (exact for bf16 values within 2^28 of
+// the unit's largest) so that each code pair is one byte permute under an f16 exponent:
+// 1024 + q exactly (see jq_gemv.h make_xstate / unit_dot).
+template <int BITS_, int GS_, int XDT_, bool F16X_ = false>
 struct Dc {
   static constexpr int BITS = BITS_, GS = GS_, XDT = XDT_;
   static constexpr int GSTEP = 128 / GS;   // groups per 128-code step
   static constexpr int TPB = 16 / GSTEP;   // activation rows per MFMA block
   static constexpr int LPG = 4 / GSTEP;    // lane groups per group
+  static constexpr bool F16X = F16X_;
+  static_assert(!F16X || (BITS == 8 && XDT == JQ_BF16), "f16-rescaled units: 8-bit, bf16 x");
   static constexpr bool SCHED = XDT == JQ_BF16 && BITS >= 2 && BITS <= 4;  // per-code offsets
-  static constexpr bool NIB = BITS == 8 && XDT == JQ_BF16;                // two nibbles
+  static constexpr bool NIB = BITS == 8 && XDT == JQ_BF16 && !F16X;       // two nibbles
   static constexpr bool TWO = !SCHED && BITS == 2;  // f16 2-bit: pairs 8 codes apart
   static constexpr uint32_t ONE2 = XDT == JQ_BF16 ? 0x3F803F80u : 0x3C003C00u;
 };
@@ -145,6 +151,10 @@ JQ_DEV Bases<D> make_bases() {
         r.v[i] = r.v[base_rep<D::BITS>(i)];
       }
     }
+  } else if constexpr (D::F16X) {
+    // exponent byte of f16 1024, beside each code byte of a pair
+    r.v[0] = 0x64646464u;
+    asm volatile("" : "+v"(r.v[0]));
   } else if constexpr (!D::NIB) {
     // The single magic base of the unscheduled forms, also pinned in a register.
     r.v[0] = Magic<D::XDT, D::BITS>::base;

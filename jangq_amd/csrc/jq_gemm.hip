@@ -42,6 +42,7 @@ struct Dg {
   static constexpr int BITS = BITS_, XDT = XDT_, GS = 64;
   static constexpr bool SCHED = false;
   static constexpr bool NIB = false;
+  static constexpr bool F16X = false;
   static constexpr bool TWO = BITS == 2;
   static constexpr uint32_t ONE2 = XDT == JQ_BF16 ? 0x3F803F80u : 0x3C003C00u;
   static constexpr float OFF = (float)(1 << BITS);

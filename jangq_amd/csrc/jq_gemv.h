@@ -21,6 +21,7 @@ constexpr int units_per_chunk() {
 struct XState {
   uint32_t pr[16];
   float X, O;
+  float scl;  // F16X: 2^-k, the unit's rescaling undone (1 otherwise)
 };
 
 template <class D, int F, int P>
@@ -30,51 +31,88 @@ JQ_DEV uint32_t xpair_of(const jqd::XRaw& r) {
 
 template <class D>
 JQ_DEV void make_xstate(const jqd::XRaw& r, XState& xs) {
-#define JQ_XP(F, P) xs.pr[4 * F + P] = xpair_of<D, F, P>(r);
-  JQ_XP(0, 0) JQ_XP(0, 1) JQ_XP(0, 2) JQ_XP(0, 3)
-  JQ_XP(1, 0) JQ_XP(1, 1) JQ_XP(1, 2) JQ_XP(1, 3)
-  JQ_XP(2, 0) JQ_XP(2, 1) JQ_XP(2, 2) JQ_XP(2, 3)
-  JQ_XP(3, 0) JQ_XP(3, 1) JQ_XP(3, 2) JQ_XP(3, 3)
-#undef JQ_XP
-  float X = 0.f;
+  if constexpr (D::F16X) {
+    // The unit's largest bf16 exponent field e; x' = x 2^k with k = 141 - e puts the largest
+    // |x'| in [2^14, 2^15). bf16 values have 8 significant bits, so x' is exact in f16 unless
+    // it falls below f16's normal range (|x| < 2^-28 of the largest; those truncate).
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 m = {0, 0};
 #pragma unroll
-  for (int i = 0; i < 16; ++i) X = dot2<D::XDT>(r.d[i], D::ONE2, X);
-  xs.X = X;
-  if constexpr (D::SCHED) {
-    float O = 0.f;
+    for (int i = 0; i < 16; ++i)
+      m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, r.d[i] & 0x7F807F80u));
+    const int e = (int)((m[0] > m[1] ? m[0] : m[1]) >> 7);
+    const int k = 141 - e;
+    float X = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) O = dot2<D::XDT>(jqd::bo_dword<D>(i >> 2, i & 3), xs.pr[i], O);
-    xs.O = O;
-  } else if constexpr (D::NIB) {
-    xs.O = -272.f * X;
+    for (int i = 0; i < 16; ++i) {
+      const float lo = __builtin_ldexpf(__uint_as_float(r.d[i] << 16), k);
+      const float hi = __builtin_ldexpf(__uint_as_float(r.d[i] & 0xFFFF0000u), k);
+      xs.pr[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+      X = dot2<JQ_F16>(xs.pr[i], 0x3C003C00u, X);
+    }
+    xs.scl = __builtin_ldexpf(1.0f, -k);
+    xs.X = X * xs.scl;      // sum of x
+    xs.O = -1024.f * X;     // minus the codes' offset times the sum of x', in x' units
   } else {
-    xs.O = -(float)(1 << D::BITS) * X;
+    xs.scl = 1.f;
+#define JQ_XP(F, P) xs.pr[4 * F + P] = xpair_of<D, F, P>(r);
+    JQ_XP(0, 0) JQ_XP(0, 1) JQ_XP(0, 2) JQ_XP(0, 3)
+    JQ_XP(1, 0) JQ_XP(1, 1) JQ_XP(1, 2) JQ_XP(1, 3)
+    JQ_XP(2, 0) JQ_XP(2, 1) JQ_XP(2, 2) JQ_XP(2, 3)
+    JQ_XP(3, 0) JQ_XP(3, 1) JQ_XP(3, 2) JQ_XP(3, 3)
+#undef JQ_XP
+    float X = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) X = dot2<D::XDT>(r.d[i], D::ONE2, X);
+    xs.X = X;
+    if constexpr (D::SCHED) {
+      float O = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) O = dot2<D::XDT>(jqd::bo_dword<D>(i >> 2, i & 3), xs.pr[i], O);
+      xs.O = O;
+    } else if constexpr (D::NIB) {
+      xs.O = -272.f * X;
+    } else {
+      xs.O = -(float)(1 << D::BITS) * X;
+    }
   }
 }
 
 // Dot product of one unit's exact code values with its paired activations.
 template <class D>
 JQ_DEV float unit_dot(const uint32_t* w, const Bases<D>& bs, const XState& xs) {
-  float d0 = 0.f, d1 = 0.f;
+  if constexpr (D::F16X) {
+    // Pair i = codes (2i, 2i+1), bytes 2(i%2), 2(i%2)+1 of word i/2, each under the f16
+    // exponent byte 0x64: 1024 + q; the x' pairs are in the same (natural) order.
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t b0 = 2 * (i & 1), sel = b0 | (4u << 8) | ((b0 + 1) << 16) | (4u << 24);
+      d = dot2<JQ_F16>(__builtin_amdgcn_perm(bs.v[0], w[i >> 1], sel), xs.pr[i], d);
+    }
+    return d;
+  } else {
+    float d0 = 0.f, d1 = 0.f;
 #define JQ_UF(F)                                                          \
-  {                                                                       \
-    u32x4 b, bh;                                                          \
-    jqd::b_frag<D, F>(w, bs, b, bh);                                      \
-    d0 = dot2<D::XDT>(b[0], xs.pr[4 * F + 0], d0);                        \
-    d0 = dot2<D::XDT>(b[1], xs.pr[4 * F + 1], d0);                        \
-    d0 = dot2<D::XDT>(b[2], xs.pr[4 * F + 2], d0);                        \
-    d0 = dot2<D::XDT>(b[3], xs.pr[4 * F + 3], d0);                        \
-    if constexpr (D::NIB) {                                               \
-      d1 = dot2<D::XDT>(bh[0], xs.pr[4 * F + 0], d1);                     \
-      d1 = dot2<D::XDT>(bh[1], xs.pr[4 * F + 1], d1);                     \
-      d1 = dot2<D::XDT>(bh[2], xs.pr[4 * F + 2], d1);                     \
-      d1 = dot2<D::XDT>(bh[3], xs.pr[4 * F + 3], d1);                     \
-    }                                                                     \
-  }
-  JQ_UF(0) JQ_UF(1) JQ_UF(2) JQ_UF(3)
+    {                                                                       \
+      u32x4 b, bh;                                                          \
+      jqd::b_frag<D, F>(w, bs, b, bh);                                      \
+      d0 = dot2<D::XDT>(b[0], xs.pr[4 * F + 0], d0);                        \
+      d0 = dot2<D::XDT>(b[1], xs.pr[4 * F + 1], d0);                        \
+      d0 = dot2<D::XDT>(b[2], xs.pr[4 * F + 2], d0);                        \
+      d0 = dot2<D::XDT>(b[3], xs.pr[4 * F + 3], d0);                        \
+      if constexpr (D::NIB) {                                               \
+        d1 = dot2<D::XDT>(bh[0], xs.pr[4 * F + 0], d1);                     \
+        d1 = dot2<D::XDT>(bh[1], xs.pr[4 * F + 1], d1);                     \
+        d1 = dot2<D::XDT>(bh[2], xs.pr[4 * F + 2], d1);                     \
+        d1 = dot2<D::XDT>(bh[3], xs.pr[4 * F + 3], d1);                     \
+      }                                                                     \
+    }
+    JQ_UF(0) JQ_UF(1) JQ_UF(2) JQ_UF(3)
 #undef JQ_UF
-  if constexpr (D::NIB) return fmaf(16.f, d1, d0);
-  return d0;
+    if constexpr (D::NIB) return fmaf(16.f, d1, d0);
+    return d0;
+  }
 }
 
 // Sum over the 64 lanes with DPP row operations; the total lands in lane 63.

@@ -291,12 +291,13 @@ int launch_m(GemvArgs& a, hipStream_t st) {
     int64_t rows = 0;
     for (int i = 0; i < a.nprob; ++i) rows += a.b.p[i].N;
     const int cpl = row_cpl(a.b.K, D::BITS);
+    using DR = typename RowD<D>::type;
     if (rows <= kFewRows) {  // short outputs (routers): one row per item, twice the waves
-      if (cpl == 1) return launch_row<D, SB, 1, 1>(a, st);
-      return launch_row<D, SB, 2, 1>(a, st);
+      if (cpl == 1) return launch_row<DR, SB, 1, 1>(a, st);
+      return launch_row<DR, SB, 2, 1>(a, st);
     }
-    if (cpl == 1) return launch_row<D, SB, 1, 2>(a, st);
-    return launch_row<D, SB, 2, 2>(a, st);
+    if (cpl == 1) return launch_row<DR, SB, 1, 2>(a, st);
+    return launch_row<DR, SB, 2, 2>(a, st);
   }
   if (a.b.M == 2) return launch_rb<D, SB, 2, 4>(a, st);
   if constexpr (!two) return launch_rb<D, SB, 4, 4>(a, st);
@@ -307,8 +308,9 @@ template <class D, int SB>
 int launch_glu(GemvArgs& a, hipStream_t st) {
   const int cpl = row_cpl(a.b.K, D::BITS);
   if (a.b.M != 1 || cpl > 2) return JQ_ERR_SHAPE;
-  if (cpl == 1) return launch_row<D, SB, 1, 2, true>(a, st);
-  return launch_row<D, SB, 2, 2, true>(a, st);
+  using DR = typename RowD<D>::type;
+  if (cpl == 1) return launch_row<DR, SB, 1, 2, true>(a, st);
+  return launch_row<DR, SB, 2, 2, true>(a, st);
 }
 
 // The group size is a run-time argument of these kernels; D::GS is 32 only for codes in

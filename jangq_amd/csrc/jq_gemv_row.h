@@ -46,6 +46,17 @@ JQ_DEV void row_load_chunk(Rsrc r, uint32_t voff, uint32_t* w) {
   }
 }
 
+// The decode type of the row body: 8-bit codes with bf16 activations take the f16-rescaled
+// units (one byte permute per code pair instead of two nibble passes).
+template <class D>
+struct RowD {
+  using type = D;
+};
+template <int GS>
+struct RowD<jqd::Dc<8, GS, JQ_BF16>> {
+  using type = jqd::Dc<8, GS, JQ_BF16, true>;
+};
+
 // Launch arguments: problems of one grouped launch share x, M, K and the dtypes; their row
 // blocks are numbered 0 .. rb_begin[nprob) in problem order.
 struct GemvArgs {
@@ -203,7 +214,8 @@ JQ_DEV void gemv_row_body(const GemvArgs& a, int it, int nwaves, const Fin& fin)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         *(u32x4*)&xsh[ut][4 * i] = u32x4{t.pr[4 * i], t.pr[4 * i + 1], t.pr[4 * i + 2], t.pr[4 * i + 3]};
-      *(u32x4*)&xsh[ut][16] = u32x4{__float_as_uint(t.X), __float_as_uint(t.O), 0u, 0u};
+      *(u32x4*)&xsh[ut][16] = u32x4{__float_as_uint(t.X), __float_as_uint(t.O),
+                                    __float_as_uint(t.scl), 0u};
     }
     __syncthreads();
     if (!has) return;
@@ -221,6 +233,7 @@ JQ_DEV void gemv_row_body(const GemvArgs& a, int it, int nwaves, const Fin& fin)
         const u32x4 v = *(const u32x4*)&xsh[u][16];
         xs[j][t].X = __uint_as_float(v[0]);
         xs[j][t].O = __uint_as_float(v[1]);
+        xs[j][t].scl = __uint_as_float(v[2]);
       }
   } else {
 #pragma unroll
@@ -264,9 +277,10 @@ JQ_DEV void gemv_row_body(const GemvArgs& a, int it, int nwaves, const Fin& fin)
         } else {
 #pragma unroll
           for (int t = 0; t < UPL; ++t) {
-            const float sv = sb_to_f32<SB>(ring[r][j].s[t]);
+            float sv = sb_to_f32<SB>(ring[r][j].s[t]);
             const float bv = sb_to_f32<SB>(ring[r][j].b[t]);
             const float d = unit_dot<D>(ring[r][j].w + t * BITS, bs, xs[j][t]);
+            if constexpr (D::F16X) sv *= xs[j][t].scl;  // d and O are in x' units
             acc[r] = fmaf(sv, d + xs[j][t].O, fmaf(bv, xs[j][t].X, acc[r]));
           }
         }

@@ -22,8 +22,8 @@ int gu_shared(FusedGuArgs& a, int bits_s, int cpls, int kwR, int64_t itemsA, dou
               int64_t wavesB, double bytesB, hipStream_t st) {
 #define JQ_GU(BS, C)                                                                       \
   if (bits_s == BS && cpls == C)                                                           \
-    return gu_launch<DR, RW, jqd::Dc<BS, 64, JQ_BF16>, C>(a, kwR, itemsA, bytesA, wavesB,  \
-                                                          bytesB, st);
+    return gu_launch<DR, RW, typename RowD<jqd::Dc<BS, 64, JQ_BF16>>::type, C>(            \
+        a, kwR, itemsA, bytesA, wavesB, bytesB, st);
   JQ_GU(8, 2) JQ_GU(8, 1) JQ_GU(4, 2) JQ_GU(4, 1)
 #undef JQ_GU
   return JQ_ERR_SHAPE;

@@ -44,6 +44,7 @@ struct Cfg {
   static constexpr int GT = KT / GS;          // groups per k-tile
   static constexpr int SPG = GS / 32;         // MFMA slices per group
   static constexpr bool NIB = (BITS == 8 && XDT == JQ_BF16);
+  static constexpr bool F16X = false;
   static constexpr int XCH = BM * (KT / 8);   // 16-byte activation chunks per tile
   static constexpr int XIT = (XCH + 255) / 256;
   static constexpr int CVEC = BN * WPR / 4;   // 16-byte code vectors per tile
