@@ -108,3 +108,36 @@ def test_long_2bit_rows(K, N, gs):
     x = O.round_bf16(rng.standard_normal((1, K), dtype=np.float32))
     y = jq.quantized_matmul(to_tensor(x, "bf16"), q.dw, q.ds, q.db, True, gs, 2)
     _check(y, x, q, N, f"long 2-bit K{K} N{N} g{gs}")
+
+
+@pytest.mark.parametrize("N", [96, 20000])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_8bit_f16_units_dynamic_range(N, gs):
+    """8-bit codes with bf16 activations rescale each 32-value unit by a power of two into f16:
+    units scaled from 2^-60 to 2^0, values spread over 2^-20 .. 1 inside a unit, an all-zero
+    unit and a single-value unit; per-wave (N = 96) and block-shared (N = 20000) state. (The
+    largest scale stays at 1: the north-star max-abs bound is absolute, and outputs far above
+    1 carry fp32 accumulation noise beyond it on any kernel.)"""
+    K = 4096
+    print(f"8-bit f16 units N{N} g{gs}", flush=True)
+    q = RandQ(N, K, 8, gs, seed=780 + gs + N % 7)
+    rng = np.random.default_rng(781)
+    units = K // 32
+    x = rng.standard_normal((1, K)).astype(np.float64)
+    x *= np.repeat(2.0 ** rng.integers(-60, 1, units), 32)[None, :]           # per-unit scale
+    x *= 2.0 ** rng.integers(-20, 1, (1, K))                                   # spread in a unit
+    x[:, 32 * 5:32 * 6] = 0.0                                                  # an all-zero unit
+    x[:, 32 * 9 + 1:32 * 10] = 0.0                                             # one value left
+    x = O.round_bf16(x.astype(np.float32))
+    y = jq.quantized_matmul(to_tensor(x, "bf16"), q.dw, q.ds, q.db, True, gs, 8)
+    _check(y, x, q, N, f"8-bit f16 units N{N} g{gs}")
+    # the SwiGLU pair (the shared expert's form) on the same activations
+    u = RandQ(N, K, 8, gs, seed=782 + gs)
+    h = values_of(jq.quantized_swiglu(to_tensor(x, "bf16"), (q.dw, q.ds, q.db, 8),
+                                      (u.dw, u.ds, u.db, 8), gs))
+    for rows in _slices(N, 512):
+        gv = O.round_bf16(x.astype(np.float64) @ _deq(q, rows).T).astype(np.float64)
+        uv = O.round_bf16(x.astype(np.float64) @ _deq(u, rows).T).astype(np.float64)
+        ref = O.silu(gv) * uv
+        assert_close(h[:, rows], O.round_bf16(ref), f"8-bit swiglu N{N} g{gs} rows {rows.start}",
+                     exact=ref, out_dtype="bf16", ulps=1)
