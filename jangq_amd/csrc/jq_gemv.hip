@@ -225,10 +225,12 @@ int launch_row(GemvArgs& a, hipStream_t st) {
   };
   // Waves with several items build the activation state once per block (measured at config 2:
   // gate|up, 3 items per wave, 13.0 -> 12.6 us); with one item per wave the barrier is only
-  // latency (q|k|v, o and config 1 each 0.1-0.2 us slower), so every wave builds its own.
+  // latency (q|k|v, o and config 1 each 0.1-0.2 us slower), so every wave builds its own,
+  // except for the f16-rescaled 8-bit units, whose state costs about twice as much to build
+  // (config-5 8-bit attention T=1 14.5 -> 14.1 us, the config-5 layer T=1 41.3 -> 40.7 us).
   int64_t waves = 0, iters = 0;
   shape(gemv_row_kernel<D, SB, CPL, RB, GLU, false>, waves, iters);
-  if (iters >= 2) {
+  if (iters >= 2 || D::F16X) {
     shape(gemv_row_kernel<D, SB, CPL, RB, GLU, true>, waves, iters);
     gemv_row_kernel<D, SB, CPL, RB, GLU, true><<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(a);
   } else {
