@@ -69,10 +69,12 @@ constexpr const Sched& sched() {
   else return kSched4;
 }
 
-// F16X_ (the vector-ALU row GEMV only, 8-bit codes, bf16 activations): the activations are
-// rescaled per 32-code unit by a power of two into f16 (exact for bf16 values within 2^28 of
-// the unit's largest) so that each code pair is one byte permute under an f16 exponent:
-// 1024 + q exactly (see jq_gemv.h make_xstate / unit_dot).
+// F16X_ (the vector-ALU row GEMV only, 6- and 8-bit codes, bf16 activations): the
+// activations are rescaled per 32-code unit by a power of two into f16 (exact for bf16 values
+// within 2^28 of the unit's largest), so that a code pair becomes one f16 pair with one
+// instruction: a byte permute under the exponent of 1024 (8-bit: 1024 + q), or an and-or of a
+// funnel-shifted window (6-bit, codes a and a + 2: 64 + q_a and 1024 + q_{a+2}) (see jq_gemv.h
+// make_xstate / unit_dot).
 template <int BITS_, int GS_, int XDT_, bool F16X_ = false>
 struct Dc {
   static constexpr int BITS = BITS_, GS = GS_, XDT = XDT_;
@@ -80,7 +82,8 @@ struct Dc {
   static constexpr int TPB = 16 / GSTEP;   // activation rows per MFMA block
   static constexpr int LPG = 4 / GSTEP;    // lane groups per group
   static constexpr bool F16X = F16X_;
-  static_assert(!F16X || (BITS == 8 && XDT == JQ_BF16), "f16-rescaled units: 8-bit, bf16 x");
+  static_assert(!F16X || ((BITS == 6 || BITS == 8) && XDT == JQ_BF16),
+                "f16-rescaled units: 6- or 8-bit codes, bf16 x");
   static constexpr bool SCHED = XDT == JQ_BF16 && BITS >= 2 && BITS <= 4;  // per-code offsets
   static constexpr bool NIB = BITS == 8 && XDT == JQ_BF16 && !F16X;       // two nibbles
   static constexpr bool TWO = !SCHED && BITS == 2;  // f16 2-bit: pairs 8 codes apart
@@ -152,8 +155,9 @@ JQ_DEV Bases<D> make_bases() {
       }
     }
   } else if constexpr (D::F16X) {
-    // exponent byte of f16 1024, beside each code byte of a pair
-    r.v[0] = 0x64646464u;
+    // 8-bit: the exponent byte of f16 1024 beside each code byte of a pair; 6-bit: the f16
+    // exponents of 64 (lo half, code at mantissa bit 4) and 1024 (hi half, bit 0)
+    r.v[0] = D::BITS == 8 ? 0x64646464u : ((21u << 10) | (25u << 26));
     asm volatile("" : "+v"(r.v[0]));
   } else if constexpr (!D::NIB) {
     // The single magic base of the unscheduled forms, also pinned in a register.

@@ -52,7 +52,25 @@ JQ_DEV void make_xstate(const jqd::XRaw& r, XState& xs) {
     }
     xs.scl = __builtin_ldexpf(1.0f, -k);
     xs.X = X * xs.scl;      // sum of x
-    xs.O = -1024.f * X;     // minus the codes' offset times the sum of x', in x' units
+    if constexpr (D::BITS == 8) {
+      xs.O = -1024.f * X;   // minus the codes' offset times the sum of x', in x' units
+    } else {
+      // 6-bit pairs (a, a + 2), a = 4m or 4m + 1: (x'_4m, x'_4m+2) are the low halves of
+      // dwords 2m, 2m+1, (x'_4m+1, x'_4m+3) the high halves; offsets 64 (a) and 1024 (a + 2)
+      uint32_t q[16];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        q[2 * m] = __builtin_amdgcn_perm(xs.pr[2 * m + 1], xs.pr[2 * m], 0x05040100u);
+        q[2 * m + 1] = __builtin_amdgcn_perm(xs.pr[2 * m + 1], xs.pr[2 * m], 0x07060302u);
+      }
+      float O = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        xs.pr[i] = q[i];
+        O = dot2<JQ_F16>(q[i], 0xE400D400u, O);  // f16 (-64, -1024)
+      }
+      xs.O = O;
+    }
   } else {
     xs.scl = 1.f;
 #define JQ_XP(F, P) xs.pr[4 * F + P] = xpair_of<D, F, P>(r);
@@ -82,13 +100,29 @@ JQ_DEV void make_xstate(const jqd::XRaw& r, XState& xs) {
 template <class D>
 JQ_DEV float unit_dot(const uint32_t* w, const Bases<D>& bs, const XState& xs) {
   if constexpr (D::F16X) {
-    // Pair i = codes (2i, 2i+1), bytes 2(i%2), 2(i%2)+1 of word i/2, each under the f16
-    // exponent byte 0x64: 1024 + q; the x' pairs are in the same (natural) order.
     float d = 0.f;
+    if constexpr (D::BITS == 8) {
+      // Pair i = codes (2i, 2i+1), bytes 2(i%2), 2(i%2)+1 of word i/2, each under the f16
+      // exponent byte 0x64: 1024 + q; the x' pairs are in the same (natural) order.
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const uint32_t b0 = 2 * (i & 1), sel = b0 | (4u << 8) | ((b0 + 1) << 16) | (4u << 24);
-      d = dot2<JQ_F16>(__builtin_amdgcn_perm(bs.v[0], w[i >> 1], sel), xs.pr[i], d);
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t b0 = 2 * (i & 1), sel = b0 | (4u << 8) | ((b0 + 1) << 16) | (4u << 24);
+        d = dot2<JQ_F16>(__builtin_amdgcn_perm(bs.v[0], w[i >> 1], sel), xs.pr[i], d);
+      }
+    } else {
+      // Pair i = codes (a, a + 2), a = 4(i/2) + i%2: the 32-bit window of the unit starting
+      // at bit 6a - 4 holds code a at bits 4..9 and code a + 2 at bits 16..21.
+#define JQ_P6(I)                                                                         \
+  {                                                                                      \
+    constexpr int a = 4 * (I >> 1) + (I & 1), s = 6 * a - 4;                             \
+    uint32_t win;                                                                        \
+    if constexpr (s < 0) win = w[0] << (-s);                                             \
+    else win = jqd::window<6, (s < 0 ? 0 : s)>(w);                                       \
+    d = dot2<JQ_F16>((win & 0x003F03F0u) | bs.v[0], xs.pr[I], d);                        \
+  }
+      JQ_P6(0) JQ_P6(1) JQ_P6(2) JQ_P6(3) JQ_P6(4) JQ_P6(5) JQ_P6(6) JQ_P6(7)
+      JQ_P6(8) JQ_P6(9) JQ_P6(10) JQ_P6(11) JQ_P6(12) JQ_P6(13) JQ_P6(14) JQ_P6(15)
+#undef JQ_P6
     }
     return d;
   } else {

@@ -46,8 +46,8 @@ JQ_DEV void row_load_chunk(Rsrc r, uint32_t voff, uint32_t* w) {
   }
 }
 
-// The decode type of the row body: 8-bit codes with bf16 activations take the f16-rescaled
-// units (one byte permute per code pair instead of two nibble passes).
+// The decode type of the row body: 6- and 8-bit codes with bf16 activations take the
+// f16-rescaled units (one instruction per code pair).
 template <class D>
 struct RowD {
   using type = D;
@@ -55,6 +55,10 @@ struct RowD {
 template <int GS>
 struct RowD<jqd::Dc<8, GS, JQ_BF16>> {
   using type = jqd::Dc<8, GS, JQ_BF16, true>;
+};
+template <int GS>
+struct RowD<jqd::Dc<6, GS, JQ_BF16>> {
+  using type = jqd::Dc<6, GS, JQ_BF16, true>;
 };
 
 // Launch arguments: problems of one grouped launch share x, M, K and the dtypes; their row
