@@ -266,14 +266,26 @@ int check_expert_shape(int bits, int gs, int64_t E, int64_t N, int64_t K) {
   return JQ_OK;
 }
 
-// The MoE combine (jqk::MoeCombine) of y [T, k, H] (slot outputs already rounded).
-// One thread per 8 consecutive elements of a row (H % 8 == 0) or per element.
-template <int DT, int VEC>
+// The MoE combine (jqk::MoeCombine) of y [T, k, H] (slot outputs already rounded). One thread
+// per two consecutive elements of a row (PAIR: 16-bit types, H even; one 32-bit load per slot)
+// or per element; the slots summed in slot order in fp32 as before. With eight elements per
+// thread (scalar 16-bit loads) config 5 at T = 32 ran 64 blocks for 14.1 us.
+template <int DT, bool PAIR>
 __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ y,
                                                       jqk::MoeCombine c, int64_t T, int k,
                                                       int64_t H) {
+  constexpr int VEC = PAIR ? 2 : 1;
   const int64_t per_row = H / VEC;
   const int64_t n = T * per_row;
+  auto ld = [&](const void* p, int64_t e, float (&v)[VEC]) {
+    if constexpr (PAIR) {
+      const uint32_t w = ((const uint32_t*)p)[e >> 1];
+      v[0] = DT == JQ_BF16 ? bf16_bits_to_f32(w & 0xFFFFu) : f16_bits_to_f32((uint16_t)w);
+      v[1] = DT == JQ_BF16 ? bf16_bits_to_f32(w >> 16) : f16_bits_to_f32((uint16_t)(w >> 16));
+    } else {
+      v[0] = load_t<DT>(p, e);
+    }
+  };
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = i / per_row, col = (i - t * per_row) * VEC;
@@ -282,19 +294,21 @@ __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ y
     for (int v = 0; v < VEC; ++v) acc[v] = 0.f;
     for (int j = 0; j < k; ++j) {
       const float wj = c.before ? 1.f : c.w[t * k + j];
-      const int64_t base = (t * k + j) * H + col;
+      float yv[VEC];
+      ld(y, (t * k + j) * H + col, yv);
 #pragma unroll
-      for (int v = 0; v < VEC; ++v)
-        acc[v] = c.before ? acc[v] + load_t<DT>(y, base + v) : fmaf(wj, load_t<DT>(y, base + v), acc[v]);
+      for (int v = 0; v < VEC; ++v) acc[v] = c.before ? acc[v] + yv[v] : fmaf(wj, yv[v], acc[v]);
     }
     const float gl = c.shared_gate ? load_t<DT>(c.shared_gate, t) : 0.f;
+    float sh[VEC];
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      const float sh = c.shared ? load_t<DT>(c.shared, t * H + col + v) : 0.f;
+    for (int v = 0; v < VEC; ++v) sh[v] = 0.f;
+    if (c.shared) ld(c.shared, t * H + col, sh);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
       store_t<DT>(c.out, t * H + col + v,
-                  jqk::moe_final(c.before, acc[v], c.shared != nullptr, sh,
+                  jqk::moe_final(c.before, acc[v], c.shared != nullptr, sh[v],
                                  c.shared_gate != nullptr, gl, DT));
-    }
   }
 }
 
@@ -354,15 +368,18 @@ extern "C" {
 
 static int combine_launch(const void* y, const jqk::MoeCombine& c, int64_t T, int k, int64_t H,
                           int dtype, hipStream_t st) {
-  const bool vec = H % 8 == 0;
-  const int64_t n = T * (vec ? H / 8 : H);
-#define JQ_C(DT)                                                                  \
-  if (vec) combine_kernel<DT, 8><<<grid_for(n), 256, 0, st>>>(y, c, T, k, H);    \
-  else combine_kernel<DT, 1><<<grid_for(n), 256, 0, st>>>(y, c, T, k, H);
-  if (dtype == JQ_BF16) { JQ_C(JQ_BF16) }
-  else if (dtype == JQ_F16) { JQ_C(JQ_F16) }
-  else { JQ_C(JQ_F32) }
-#undef JQ_C
+  // (16-bit pairs need an even H and 4-byte aligned rows; the buffers are 16-byte aligned)
+  const bool pair = dtype != JQ_F32 && H % 2 == 0;
+  const int64_t n = T * (pair ? H / 2 : H);
+  if (dtype == JQ_BF16) {
+    if (pair) combine_kernel<JQ_BF16, true><<<grid_for(n), 256, 0, st>>>(y, c, T, k, H);
+    else combine_kernel<JQ_BF16, false><<<grid_for(n), 256, 0, st>>>(y, c, T, k, H);
+  } else if (dtype == JQ_F16) {
+    if (pair) combine_kernel<JQ_F16, true><<<grid_for(n), 256, 0, st>>>(y, c, T, k, H);
+    else combine_kernel<JQ_F16, false><<<grid_for(n), 256, 0, st>>>(y, c, T, k, H);
+  } else {
+    combine_kernel<JQ_F32, false><<<grid_for(n), 256, 0, st>>>(y, c, T, k, H);
+  }
   return jqh::launch_status();
 }
 
