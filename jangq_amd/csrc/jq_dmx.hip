@@ -160,7 +160,12 @@ JQ_DEV void lane_toks(const GatherPlan& pl, int4 tl, int xt, int lg, LaneToks<TP
 
 // SPLIT (dense, one problem): unit u of the item walk is a K chunk of a.split steps; its
 // partial sums go to a.part and a second kernel adds the chunks.
-template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB, bool SPLIT = false>
+// DGLU (dense, problems 0 = gate and 1 = up of one shape): items alternate gate and up of one
+// row block (item 2j: gate rows of block j, 2j + 1: up rows), both in the same block; the
+// reducing wave of an output keeps the rounded gate value in a register and the up item
+// stores silu(g) * u (glu_value with a.g[0].glu_limit) into problem 0's output.
+template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB, bool SPLIT = false,
+          bool DGLU = false>
 struct Dmx {
   using R = Ring<D, RT, SW, NSLOT>;
   static constexpr int BITS = D::BITS, TPB = D::TPB, TPL = 4 / D::GSTEP;
@@ -412,7 +417,10 @@ struct Dmx {
 
   static JQ_DEV void cursor_at(const DmxArgs& a, int it, Cursor& c, int4* tlo) {
     c.it = it;
-    if constexpr (GATHER || SPLIT) {
+    if constexpr (DGLU) {
+      c.u = it & 1;
+      c.rb = it >> 1;
+    } else if constexpr (GATHER || SPLIT) {
       c.u = it / a.nrb;
       c.rb = it - c.u * a.nrb;
     } else {
@@ -429,6 +437,12 @@ struct Dmx {
   // Returns whether the unit changed.
   static JQ_DEV bool advance(const DmxArgs& a, Cursor& c, int4* tlo) {
     ++c.it;
+    if constexpr (DGLU) {
+      c.u ^= 1;
+      c.rb += c.u ^ 1;
+      unit_bases(a, c, tlo);
+      return true;
+    }
     if (++c.rb < c.nrb) return false;
     c.rb = 0;
     ++c.u;
@@ -457,7 +471,8 @@ struct Dmx {
                          JQ_LDS uint8_t* __restrict__ ring1, JQ_LDS uint8_t* __restrict__ ring2,
                          JQ_LDS uint8_t* __restrict__ ring3, JQ_LDS float* __restrict__ red) {
     const int items = GATHER ? ldc(a.plan.n_tiles) * a.nrb : a.items;
-    const int per = (items + (int)gridDim.x - 1) / (int)gridDim.x;
+    int per = (items + (int)gridDim.x - 1) / (int)gridDim.x;
+    if constexpr (DGLU) per += per & 1;  // whole (gate, up) pairs per block
     const int first = blockIdx.x * per;
     const int end = first + per < items ? first + per : items;
     if (first >= end) return;  // whole block
@@ -497,6 +512,7 @@ struct Dmx {
                [&](int t, int64_t& row) { row = pm0 + t; return t < pmr; }, ac);
     }
     const Bases<D> bs = make_bases<D>();
+    float gk[NOUT];  // DGLU: rounded gate values of the wave's outputs, kept for the up item
 
     auto step = [&](int it, JQ_LDS uint8_t* __restrict__ cur, JQ_LDS uint8_t* __restrict__ fill) {
       const int par = (it - first) & 1;  // partials double-buffered across consecutive items
@@ -527,7 +543,31 @@ struct Dmx {
       // Sum the waves' partials and store: output slot o = (ab, r, k); gathered gate|up
       // pairs take r = 0 (gate) and r = 1 (up) together.
       constexpr int NO = NB == 2 ? NOUT / 2 : NOUT;
-      for (int oi = wave; oi < NO; oi += KW) {
+      if constexpr (DGLU) {
+        static_assert(RT == 1 && NB == 1 && !GATHER && !SPLIT, "dense gate|up pairs");
+        const bool up = wc.u == 1;
+#pragma unroll
+        for (int j = 0; j < NOUT; ++j) {
+          const int oi = wave + j * KW;  // output slot (ab, k) = (oi / TPL, oi % TPL)
+          if (oi < NOUT) {
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < kMaxKW; ++w)
+              if (w < KW) v += red[((par * KW + w) * NOUT + oi) * 64 + lane];
+            const float rv = round_to(v, a.yd);
+            if (!up) {
+              gk[j] = rv;
+            } else {
+              const int tok = (oi / TPL) * TPB + TPL * lg + oi % TPL;
+              const int64_t n = row0 + lr;
+              if (tok < pmr && n < wc.N)
+                store_out(a.b.p[0].y, (int64_t)(pm0 + tok) * wc.N + n,
+                          jqk::glu_value(gk[j], rv, a.g[0].glu_limit, 1.f), a.yd);
+            }
+          }
+        }
+      }
+      for (int oi = wave; oi < (DGLU ? 0 : NO); oi += KW) {
         const int k = oi % TPL;
         const int rr = NB == 2 ? 0 : (oi / TPL) % RT;
         const int ab = NB == 2 ? oi / TPL : oi / (TPL * RT);
@@ -607,9 +647,10 @@ struct Dmx {
   }
 };
 
-template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB, bool SPLIT>
+template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB, bool SPLIT,
+          bool DGLU>
 __global__ void __launch_bounds__(64 * kMaxKW) dmx_kernel(DmxArgs a) {
-  using K = Dmx<D, SB, RT, NA, SW, NSLOT, GATHER, NB, SPLIT>;
+  using K = Dmx<D, SB, RT, NA, SW, NSLOT, GATHER, NB, SPLIT, DGLU>;
   using R = typename K::R;
   extern __shared__ __attribute__((aligned(1024))) uint8_t dmx_lds[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -629,11 +670,12 @@ constexpr size_t dmx_lds_bytes(int kw) {
   return (size_t)kw * R::WAVE + (size_t)2 * kw * RT * NA * (4 / D::GSTEP) * 64 * 4;
 }
 
-template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB, bool SPLIT>
+template <class D, int SB, int RT, int NA, int SW, int NSLOT, bool GATHER, int NB, bool SPLIT,
+          bool DGLU>
 int launch_cfg(DmxArgs& a, int kw, int64_t max_items, hipStream_t st) {
   const size_t lds = dmx_lds_bytes<D, RT, NA, SW, NSLOT>(kw);
   if (lds > (size_t)kLdsMax) return JQ_ERR_SHAPE;
-  auto kern = dmx_kernel<D, SB, RT, NA, SW, NSLOT, GATHER, NB, SPLIT>;
+  auto kern = dmx_kernel<D, SB, RT, NA, SW, NSLOT, GATHER, NB, SPLIT, DGLU>;
   if (!jqh::set_lds((const void*)kern, lds)) return JQ_ERR_LAUNCH;
   int64_t cap = (int64_t)jqh::blocks_per_cu((const void*)kern, 64 * kw, lds) * jqh::cus();
   int64_t grid;
@@ -670,15 +712,16 @@ inline int dmx_sw(int K) {
   return 0;
 }
 
-template <class D, int SB, int RT, int NA, bool GATHER, int NB, bool SPLIT = false>
+template <class D, int SB, int RT, int NA, bool GATHER, int NB, bool SPLIT = false,
+          bool DGLU = false>
 int launch_sw(DmxArgs& a, int64_t max_items, hipStream_t st) {
   const int kc = SPLIT ? a.split * 128 : a.K;  // codes of K one block covers
   const int sw = dmx_sw(kc);
   const int kw = sw ? kc / 128 / sw : 0;
   if (sw == 2)
-    return launch_cfg<D, SB, RT, NA, 2, ring_slots<D, RT, NA, 2>(), GATHER, NB, SPLIT>(a, kw, max_items, st);
+    return launch_cfg<D, SB, RT, NA, 2, ring_slots<D, RT, NA, 2>(), GATHER, NB, SPLIT, DGLU>(a, kw, max_items, st);
   if (sw == 4)
-    return launch_cfg<D, SB, RT, NA, 4, ring_slots<D, RT, NA, 4>(), GATHER, NB, SPLIT>(a, kw, max_items, st);
+    return launch_cfg<D, SB, RT, NA, 4, ring_slots<D, RT, NA, 4>(), GATHER, NB, SPLIT, DGLU>(a, kw, max_items, st);
   return JQ_ERR_SHAPE;
 }
 
@@ -708,6 +751,49 @@ int dense_t(const QmvBatch& b, int nprob, int yd, hipStream_t st) {
   if (total == 0) return JQ_OK;
   if (pass > D::TPB) return launch_sw<D, SB, RT, 2, false, 1>(a, total, st);
   return launch_sw<D, SB, RT, 1, false, 1>(a, total, st);
+}
+
+// Dense gate|up pairs with the SiLU * up epilogue: items (gate, up) per 16-row block, passes
+// as in dense_t.
+template <int BITS, int GS, int XDT, int SB>
+int dense_glu_t(const QmvBatch& b, float limit, int yd, hipStream_t st) {
+  using D = Dc<BITS, GS, XDT>;
+  const int pass = b.M > D::TPB ? 2 * D::TPB : D::TPB;
+  DmxArgs a;
+  a.b = b;
+  a.nprob = 2;
+  a.mpass = pass;
+  a.mtotal = b.M;
+  a.K = b.K;
+  a.yd = yd;
+  a.nrb = 0;
+  a.split = 0;
+  a.part = nullptr;
+  a.g[0].glu_limit = limit;
+  const int nrb = (int)((b.p[0].N + 15) / 16);
+  for (int i = 0; i <= jqk::kMaxProblems; ++i) a.rb_begin[i] = i == 0 ? 0 : i == 1 ? nrb : 2 * nrb;
+  a.items = 2 * nrb;
+  if (nrb == 0) return JQ_OK;
+  if (pass > D::TPB) return launch_sw<D, SB, 1, 2, false, 1, false, true>(a, a.items, st);
+  return launch_sw<D, SB, 1, 1, false, 1, false, true>(a, a.items, st);
+}
+
+template <int XDT, int SB>
+int glu_bits(int bits, int gs, const QmvBatch& b, float limit, int yd, hipStream_t st) {
+#define JQ_D(B)                                                        \
+  switch (gs) {                                                        \
+    case 64: return dense_glu_t<B, 64, XDT, SB>(b, limit, yd, st);     \
+    default: return dense_glu_t<B, 128, XDT, SB>(b, limit, yd, st);    \
+  }
+  switch (bits) {
+    case 2: JQ_D(2)
+    case 3: JQ_D(3)
+    case 4: JQ_D(4)
+    case 5: JQ_D(5)
+    case 6: JQ_D(6)
+    default: JQ_D(8)
+  }
+#undef JQ_D
 }
 
 // Chunk partials summed in chunk order and rounded: y[m0 + m, n] = sum_c part[c, m, n].
@@ -875,6 +961,16 @@ int dmx_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, i
   }
   if (xd == JQ_BF16) return dense_bits<JQ_BF16, JQ_BF16>(bits, gs, b, nprob, yd, st);
   return dense_bits<JQ_F16, JQ_F16>(bits, gs, b, nprob, yd, st);
+}
+
+int dmx_glu_launch(const QmvBatch& b, int bits, int gs, int xd, int sb, int yd, float limit,
+                   hipStream_t st) {
+  const int64_t N = b.p[0].N;
+  if (N == 0 || b.M == 0) return JQ_OK;
+  if (b.p[1].N != N || b.p[1].x != b.p[0].x) return JQ_ERR_SHAPE;
+  if (!dmx_ok(b.M, b.K, N, bits, gs, xd, sb, 1)) return JQ_ERR_SHAPE;
+  if (xd == JQ_BF16) return glu_bits<JQ_BF16, JQ_BF16>(bits, gs, b, limit, yd, st);
+  return glu_bits<JQ_F16, JQ_F16>(bits, gs, b, limit, yd, st);
 }
 
 int64_t dmx_split_workspace(int M, int64_t K, int64_t N, int bits, int gs, int xd, int sb) {

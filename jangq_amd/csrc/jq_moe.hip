@@ -444,6 +444,19 @@ static int swiglu_run(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
     return jqk::gemv_gather_launch(g, &u, plan, 1, tr, bits, group_size, x_dtype, sb_dtype,
                                    y_dtype, st);
   }
+  // Decode batches of 5..64 rows on the matrix-core kernel: gate and up row blocks in one
+  // launch with the SiLU * up epilogue (the rows the grouped dense launch would take).
+  if (M >= 5 && M <= 64 && jqk::dmx_ok((int)M, K, N, bits, group_size, x_dtype, sb_dtype, 1)) {
+    jqk::QmvBatch b;
+    b.M = (int)M;
+    b.K = (int)K;
+    b.p[0].x = x; b.p[0].codes = gate_codes; b.p[0].scales = gate_scales;
+    b.p[0].biases = gate_biases; b.p[0].y = h; b.p[0].N = N;
+    b.p[1] = b.p[0];
+    b.p[1].codes = up_codes; b.p[1].scales = up_scales; b.p[1].biases = up_biases;
+    b.p[1].y = nullptr;
+    return jqk::dmx_glu_launch(b, bits, group_size, x_dtype, sb_dtype, y_dtype, limit, st);
+  }
   // Otherwise: gate and up in one grouped dense launch, then the elementwise SiLU * up.
   if (!up_buf) return JQ_ERR_WORKSPACE;
   const void* xs[2] = {x, x};

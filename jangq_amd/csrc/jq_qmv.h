@@ -118,13 +118,19 @@ struct QmmProblem {
 // h = silu(g) * u of a SwiGLU pair whose g and u are already rounded to the output dtype:
 // the optional clamp (jang-tools/jang_tools/dsv41/model.py:1214-1218: up = clip(up, -L, L),
 // gate = min(gate, L)) and the optional per-row factor (the routing weight, model.py:1219-1222).
+// h is rounded to fp32 here (the empty asm makes it an opaque register value): a caller that
+// rounds h to f16 at a compile-time dtype would otherwise get the last product and the f16
+// rounding fused into one v_fma_mix (one rounding instead of two), and outputs an f16 ulp
+// away from the same h computed in a kernel whose output dtype is a run-time value.
 JQ_DEV float glu_value(float g, float u, float limit, float factor) {
   if (limit > 0.f) {
     g = fminf(g, limit);
     u = fminf(fmaxf(u, -limit), limit);
   }
-  const float h = g / (1.0f + expf(-g)) * u;
-  return factor == 1.f ? h : h * factor;
+  float h = g / (1.0f + expf(-g)) * u;
+  if (factor != 1.f) h *= factor;
+  asm("" : "+v"(h));
+  return h;
 }
 
 // Decode batches on matrix cores with LDS-streamed weights (jq_dmx.hip): M <= 2*16/(128/gs),
@@ -134,6 +140,11 @@ bool dmx_ok(int M, int64_t K, int64_t maxN, int bits, int gs, int xd, int sb, in
 int dmx_tokens_per_tile(int gs);
 int dmx_launch(const QmvBatch& b, int nprob, int bits, int gs, int xd, int sb, int yd,
                hipStream_t st);
+// Gate (b.p[0]) and up (b.p[1]) of one shape over the same activations in one launch:
+// b.p[0].y = silu(round(g)) * round(u), rounded (glu_value with `limit`); same limits as
+// dmx_ok with rt = 1.
+int dmx_glu_launch(const QmvBatch& b, int bits, int gs, int xd, int sb, int yd, float limit,
+                   hipStream_t st);
 // Expert-gathered form: plan tiles (plan.tiles != NULL) of up to dmx_tokens_per_tile rows;
 // with p2, gate (p) and up (p2) rows of each tile give h = silu(g) * u.
 bool dmx_gather_ok(int64_t N, int64_t K, int bits, int gs, int xd, int sb, int nb);
@@ -222,7 +233,11 @@ JQ_DEV float moe_final(int before, float acc, bool has_shared, float sh, bool ha
   if (before) return has_shared ? acc + sh : acc;
   const float r = round_to_dtype(acc, yd);
   if (!has_shared) return r;
-  if (has_gate) sh = round_to_dtype(round_to_dtype(1.0f / (1.0f + expf(-gl)), yd) * sh, yd);
+  if (has_gate) {
+    float p = round_to_dtype(1.0f / (1.0f + expf(-gl)), yd) * sh;
+    asm("" : "+v"(p));  // an fp32 product, then its rounding (as in glu_value)
+    sh = round_to_dtype(p, yd);
+  }
   return r + sh;
 }
 

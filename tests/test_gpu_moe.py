@@ -210,7 +210,7 @@ def test_moe_combine(dt, T, k, H):
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 9])
 def test_quantized_swiglu(bits, M):
     """Dense SwiGLU pair: one gathered launch at decode sizes (M <= 4; 2-bit M <= 2), the
-    grouped dense launch + elementwise kernel above."""
+    matrix-core gate|up launch with the SiLU * up epilogue above."""
     N, K, gs = 200, 512, 64
     g = QWeight(N, K, bits, gs, seed=bits * 3)
     u = QWeight(N, K, bits, gs, seed=bits * 3 + 1)
@@ -220,6 +220,47 @@ def test_quantized_swiglu(bits, M):
     ref = O.swiglu_pair(x, (g.packed, g.s, g.b, bits), (u.packed, u.s, u.b, bits), gs)
     assert tuple(h.shape) == (M, N)
     assert_close(values_of(h), ref, f"swiglu b{bits} M{M}")
+
+
+@pytest.mark.parametrize("bits,gs,K,xdt", [(2, 128, 4096, "bf16"), (3, 64, 4096, "bf16"),
+                                           (4, 64, 2048, "f16"), (5, 128, 1024, "bf16"),
+                                           (6, 64, 4096, "bf16"), (8, 64, 4096, "bf16"),
+                                           (8, 128, 1024, "f16"), (4, 128, 512, "bf16")])
+@pytest.mark.parametrize("M", [5, 9, 16, 32, 64])
+def test_quantized_swiglu_matrix_core_pairs(bits, gs, K, xdt, M):
+    """Decode batches of 5..64 rows: gate and up row blocks alternate in one matrix-core
+    launch whose up item applies silu(round(g)) * round(u). Bit-equal to the grouped dense
+    launch followed by the elementwise kernel (the same partial sums in the same order), with
+    and without the clamp; N leaves a partial 16-row block and M a partial pass. One case is
+    also checked against the oracle on a few rows."""
+    N = 1000 + bits
+    limit = 0.0 if M % 2 == 0 else 1.0
+    print(f"swiglu matrix-core pairs b{bits} g{gs} K{K} {xdt} M{M}", flush=True)
+    g = RandQ(N, K, bits, gs, seed=900 + bits + M, sidecar=xdt)
+    u = RandQ(N, K, bits, gs, seed=901 + bits + M, sidecar=xdt)
+    rng = np.random.default_rng(902 + M)
+    x = O.round_to(rng.standard_normal((M, K), dtype=np.float32), xdt)
+    tx = to_tensor(x, xdt)
+    h = jq.quantized_swiglu(tx, (g.dw, g.ds, g.db, bits), (u.dw, u.ds, u.db, bits), gs,
+                            swiglu_limit=limit)
+    gy, uy = jq.quantized_matmul_multi(tx, [(g.dw, g.ds, g.db, gs, bits), (u.dw, u.ds, u.db, gs, bits)])
+    ref = jq.swiglu(gy, uy, limit)
+    assert tuple(h.shape) == (M, N)
+    diff = (h.view(torch.int16).int() - ref.view(torch.int16).int()).abs()
+    assert torch.equal(h, ref), (f"b{bits} g{gs} K{K} M{M}: fused differs from gate|up + swiglu "
+                                 f"in {int((diff > 0).sum())} of {diff.numel()} values, "
+                                 f"at most {int(diff.max())} ulp")
+    if bits == 3 and M == 9:
+        rows = slice(N - 40, N)
+        gw = O.dequantize_affine(*g.host(None, rows), bits, gs).astype(np.float64)
+        uw = O.dequantize_affine(*u.host(None, rows), bits, gs).astype(np.float64)
+        gv = O.round_to(x.astype(np.float64) @ gw.T, xdt).astype(np.float64)
+        uv = O.round_to(x.astype(np.float64) @ uw.T, xdt).astype(np.float64)
+        if limit > 0:
+            gv, uv = np.minimum(gv, limit), np.clip(uv, -limit, limit)
+        exact = O.silu(gv) * uv
+        assert_close(values_of(h)[:, rows], O.round_to(exact, xdt), f"swiglu pairs b{bits} M{M}",
+                     exact=exact, out_dtype=xdt, ulps=1)
 
 
 @pytest.mark.parametrize("T,k,E", [(1, 4, 128), (1, 10, 512), (2, 8, 64)])
