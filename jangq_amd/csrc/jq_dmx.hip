@@ -252,10 +252,12 @@ struct Dmx {
   }
 
   // Lane (lr, lg) of activation block ab feeds token slot ab*TPB + lr/GSTEP in the lane
-  // groups of group lr % GSTEP; other lanes read zeros.
+  // groups of group lr % GSTEP; other lanes hold zeros. Only the lanes of live token slots
+  // load (the others are masked off and send no request), so a block moves each activation
+  // value once.
   template <class XRow>
-  static JQ_DEV void load_act(const uint16_t* x, int K, int s0, int lr, int lg, XRow xrow, Act& ac) {
-    const uint16_t* zero = (const uint16_t*)kZeroRow;
+  static JQ_DEV void issue_act(const uint16_t* x, int K, int s0, int lr, int lg, XRow xrow,
+                               XRaw (&raw)[NA][SW]) {
 #pragma unroll
     for (int ab = 0; ab < NA; ++ab) {
       const int t = ab * TPB + lr / D::GSTEP;
@@ -263,20 +265,39 @@ struct Dmx {
       const bool act = (lr % D::GSTEP) == lg / D::LPG && xrow(t, row);
 #pragma unroll
       for (int d = 0; d < SW; ++d) {
-        XRaw r;
-        load_xraw(act ? x + row * K + (int64_t)(s0 + d) * 128 + 32 * lg : zero, r);
-        ac.A[ab][d][0] = a_frag<D, 0>(r);
-        ac.A[ab][d][1] = a_frag<D, 1>(r);
-        ac.A[ab][d][2] = a_frag<D, 2>(r);
-        ac.A[ab][d][3] = a_frag<D, 3>(r);
+        if (act) {
+          load_xraw(x + row * K + (int64_t)(s0 + d) * 128 + 32 * lg, raw[ab][d]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 16; ++q) raw[ab][d].d[q] = 0u;
+        }
       }
     }
+  }
+
+  static JQ_DEV void finish_act(const XRaw (&raw)[NA][SW], Act& ac) {
+#pragma unroll
+    for (int ab = 0; ab < NA; ++ab)
+#pragma unroll
+      for (int d = 0; d < SW; ++d) {
+        ac.A[ab][d][0] = a_frag<D, 0>(raw[ab][d]);
+        ac.A[ab][d][1] = a_frag<D, 1>(raw[ab][d]);
+        ac.A[ab][d][2] = a_frag<D, 2>(raw[ab][d]);
+        ac.A[ab][d][3] = a_frag<D, 3>(raw[ab][d]);
+      }
     if constexpr (PRE) {
 #pragma unroll
       for (int ab = 0; ab < NA; ++ab)
 #pragma unroll
         for (int d = 0; d < SW; ++d) sums(ac.A[ab][d], ac.X[ab][d], ac.O[ab][d]);
     }
+  }
+
+  template <class XRow>
+  static JQ_DEV void load_act(const uint16_t* x, int K, int s0, int lr, int lg, XRow xrow, Act& ac) {
+    XRaw raw[NA][SW];
+    issue_act(x, K, s0, lr, lg, xrow, raw);
+    finish_act(raw, ac);
   }
 
   // The MFMAs and scale terms of one item from its ring slot.
@@ -494,22 +515,29 @@ struct Dmx {
     int4 tl;
     cursor_at(a, first, wc, &tl);
     cc = wc;
-#pragma unroll
-    for (int k = 0; k < NSLOT - 1; ++k) {
-      ItemSrc<RT> src;
-      sources(cc, cc.it < end, rowbytes, sbrow, src);
-      copy(src, o, k == 0 ? ring0 : k == 1 ? ring1 : ring2);  // k < NSLOT - 1 <= 3
-      asm volatile("" ::: "memory");
-      advance(a, cc, nullptr);
-    }
+    // The first item's activations are requested before the ring's first copies and turned
+    // into A fragments after them, so that both round trips overlap.
     Act ac;
     LaneToks<TPL> tk;
-    if constexpr (GATHER) {
-      lane_toks<MP, TPL>(a.plan, tl, lr / D::GSTEP, lg, tk);
-      load_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg, [&](int, int64_t& row) { row = tk.xrow; return tk.xlive; }, ac);
-    } else {
-      load_act((const uint16_t*)a.b.p[0].x, a.K, s0 + (SPLIT ? wc.u * a.split : 0), lr, lg,
-               [&](int t, int64_t& row) { row = pm0 + t; return t < pmr; }, ac);
+    {
+      XRaw raw[NA][SW];
+      if constexpr (GATHER) {
+        lane_toks<MP, TPL>(a.plan, tl, lr / D::GSTEP, lg, tk);
+        issue_act((const uint16_t*)a.g[0].x, a.K, s0, lr, lg,
+                  [&](int, int64_t& row) { row = tk.xrow; return tk.xlive; }, raw);
+      } else {
+        issue_act((const uint16_t*)a.b.p[0].x, a.K, s0 + (SPLIT ? wc.u * a.split : 0), lr, lg,
+                  [&](int t, int64_t& row) { row = pm0 + t; return t < pmr; }, raw);
+      }
+#pragma unroll
+      for (int k = 0; k < NSLOT - 1; ++k) {
+        ItemSrc<RT> src;
+        sources(cc, cc.it < end, rowbytes, sbrow, src);
+        copy(src, o, k == 0 ? ring0 : k == 1 ? ring1 : ring2);  // k < NSLOT - 1 <= 3
+        asm volatile("" ::: "memory");
+        advance(a, cc, nullptr);
+      }
+      finish_act(raw, ac);
     }
     const Bases<D> bs = make_bases<D>();
     float gk[NOUT];  // DGLU: rounded gate values of the wave's outputs, kept for the up item
