@@ -171,7 +171,11 @@ struct Dmx {
   static constexpr int BITS = D::BITS, TPB = D::TPB, TPL = 4 / D::GSTEP;
   static constexpr int MP = NA * TPB;            // token slots of a pass or tile
   static constexpr int NOUT = RT * NA * TPL;     // partial outputs per lane per item
-  static constexpr bool PRE = NA * SW <= 4;      // X and O kept per step in registers
+  // X and O kept per step in registers: always up to 4 steps of activation blocks, and up to
+  // 8 in the plain dense form at <= 6 bits (<= 5 with the K split), where the gfx950 build's
+  // resource report shows no spill; elsewhere they are recomputed per item.
+  static constexpr bool PRE =
+      NA * SW <= 4 || (NA * SW <= 8 && !GATHER && !DGLU && BITS <= (SPLIT ? 5 : 6));
 
   // Per-lane byte offsets of the copies inside a tile's rows (the same for every item):
   // copy j, lane i lands at LDS byte 1024 j + 16 i of the tile = (row f / RS, byte f % RS);
