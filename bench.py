@@ -39,10 +39,12 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true")
     p.add_argument("--only", default="", help="comma list of extra workloads to run")
-    p.add_argument("--profile", choices=("gateup", "copy", "down", "c1", "c3", "c5"),
+    p.add_argument("--profile", choices=("gateup", "gateup8", "gateup32", "copy", "down", "c1",
+                                         "c3", "c5"),
                    default=None,
                    help="run one workload eagerly for rocprofv3 counter passes and print one "
-                        "JSON line: the gate|up launch (gateup), a plain 256 MiB copy (copy), "
+                        "JSON line: the gate|up launch (gateup; at batch 8 / 32: gateup8, "
+                        "gateup32), a plain 256 MiB copy (copy), "
                         "the 2-bit down projection (down), config 1 (c1), or the MoE layer of "
                         "config 3 / 5 at T = 1 (c3, c5)")
     return p.parse_args()
@@ -500,7 +502,9 @@ def profile_run(kind, steps):
         return {"profile": kind, "algorithmic_bytes": w.nbytes() + 2 * K + 2 * N,
                 "launches": steps, "copies": R}
 
-    layer, acts, _, _ = c2_block(gen, 1)
+    # gate|up of the config-2 block at batch 1 (gateup), 8 or 32 (gateup8 / gateup32)
+    M = {"gateup": 1, "gateup8": 8, "gateup32": 32}[kind]
+    layer, acts, _, _ = c2_block(gen, M)
     R = copies_for(layer["g"].nbytes() + layer["u"].nbytes())
     gs = [(layer["g"], layer["u"])] + [(layer["g"].clone(), layer["u"].clone())
                                       for _ in range(R - 1)]
@@ -509,8 +513,8 @@ def profile_run(kind, steps):
         jq.quantized_matmul_multi(acts[0], [g.tup(), u.tup()])
     torch.cuda.synchronize()
     x = acts[0]
-    nb = layer["g"].nbytes() + layer["u"].nbytes() + 2 * x.numel() + 2 * 2 * 14336
-    return {"profile": "gateup", "algorithmic_bytes": nb, "launches": steps, "copies": R}
+    nb = layer["g"].nbytes() + layer["u"].nbytes() + 2 * x.numel() + 2 * 2 * M * 14336
+    return {"profile": kind, "algorithmic_bytes": nb, "launches": steps, "copies": R}
 
 
 # ----------------------------------------------------------------------------- main
