@@ -757,12 +757,19 @@ int launch_sw(DmxArgs& a, int64_t max_items, hipStream_t st) {
   return JQ_ERR_SHAPE;
 }
 
-// Dense: passes of TPB (one activation block) or 2 TPB rows, all in one launch.
+// Dense: passes of TPB (one activation block) or 2 TPB rows, all in one launch. Passes of
+// one block are taken when every (pass, row block) item still gets a CU of its own (short
+// outputs such as a router: the one-block form keeps its activation sums in registers, and
+// the extra passes run on CUs that would sit idle).
 template <int BITS, int GS, int XDT, int SB>
 int dense_t(const QmvBatch& b, int nprob, int yd, hipStream_t st) {
   using D = Dc<BITS, GS, XDT>;
   constexpr int RT = 1;
-  const int pass = b.M > D::TPB ? 2 * D::TPB : D::TPB;
+  int64_t rows16 = 0;
+  for (int i = 0; i < nprob; ++i) rows16 += (b.p[i].N + 15) / 16;
+  const int64_t passes1 = (b.M + D::TPB - 1) / D::TPB;
+  const bool wide = b.M > D::TPB && rows16 * passes1 > jqh::cus();
+  const int pass = wide ? 2 * D::TPB : D::TPB;
   DmxArgs a;
   a.b = b;
   a.nprob = nprob;
