@@ -373,9 +373,9 @@ int jq_moe_experts(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, 
  * h rounded to y_dtype. Gate and up share bits, group size, N and K.
  * up_buf: caller scratch of M*N elements of y_dtype, required when M is above the decode
  * sizes (M > 4; 2-bit: M > 2); NULL is accepted for decode sizes (one launch, no scratch).
- * At 5..64 rows with K <= 4096, group size 64 or 128 and x and scales of one 16-bit dtype
- * the pair also runs as one launch (matrix-core kernel with the SiLU * up epilogue) and
- * leaves up_buf untouched.
+ * At 5..64 rows with K <= 4096, group size 64 or 128 and x and scales of one 16-bit dtype,
+ * for 8-bit codes or at most 16 / (128 / group_size) rows, the pair also runs as one launch
+ * (matrix-core kernel with the SiLU * up epilogue) and leaves up_buf untouched.
  * No MLX operator as one call: replaces gate_proj(x), up_proj(x) and silu(g) * u of the
  * shared-expert MLP (jang-tools/jang_tools/qwen4_exp/modeling.py:597,
  * jang-tools/jang_tools/dsv41/metal_decode.py:355-371 for the shared slot).

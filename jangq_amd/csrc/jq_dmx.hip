@@ -389,6 +389,7 @@ struct Dmx {
     const char* cb[RT];     // codes of the unit's row 0 (per tile)
     const char* sb[RT];     // scales
     const char* bb[RT];     // biases
+    const char *ocb, *osb, *obb;  // DGLU: the other unit's codes, scales and biases
   };
 
   static JQ_DEV void unit_bases(const DmxArgs& a, Cursor& c, int4* tlo) {
@@ -445,6 +446,10 @@ struct Dmx {
     if constexpr (DGLU) {
       c.u = it & 1;
       c.rb = it >> 1;
+      const QmvProblem& po = a.b.p[c.u ^ 1];
+      c.ocb = (const char*)po.codes;
+      c.osb = (const char*)po.scales;
+      c.obb = (const char*)po.biases;
     } else if constexpr (GATHER || SPLIT) {
       c.u = it / a.nrb;
       c.rb = it - c.u * a.nrb;
@@ -463,9 +468,12 @@ struct Dmx {
   static JQ_DEV bool advance(const DmxArgs& a, Cursor& c, int4* tlo) {
     ++c.it;
     if constexpr (DGLU) {
+      // gate and up share N: swap the two units' bases instead of reading them again
       c.u ^= 1;
       c.rb += c.u ^ 1;
-      unit_bases(a, c, tlo);
+      const char* t = c.cb[0]; c.cb[0] = c.ocb; c.ocb = t;
+      t = c.sb[0]; c.sb[0] = c.osb; c.osb = t;
+      t = c.bb[0]; c.bb[0] = c.obb; c.obb = t;
       return true;
     }
     if (++c.rb < c.nrb) return false;

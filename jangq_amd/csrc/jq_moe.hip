@@ -445,8 +445,13 @@ static int swiglu_run(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
                                    y_dtype, st);
   }
   // Decode batches of 5..64 rows on the matrix-core kernel: gate and up row blocks in one
-  // launch with the SiLU * up epilogue (the rows the grouped dense launch would take).
-  if (M >= 5 && M <= 64 && jqk::dmx_ok((int)M, K, N, bits, group_size, x_dtype, sb_dtype, 1)) {
+  // launch with the SiLU * up epilogue (the rows the grouped dense launch would take), at
+  // 8 bits or in passes of one activation block. At <= 6 bits with two-block passes the
+  // grouped launch keeps its activation sums in registers, which the gate|up form cannot
+  // without spilling: there the two launches are faster (3-bit 2 x 14336 x 4096 at 32 rows
+  // 33.9 against 44.5 us).
+  if (M >= 5 && M <= 64 && (bits > 6 || M <= jqk::dmx_tokens_per_tile(group_size)) &&
+      jqk::dmx_ok((int)M, K, N, bits, group_size, x_dtype, sb_dtype, 1)) {
     jqk::QmvBatch b;
     b.M = (int)M;
     b.K = (int)K;

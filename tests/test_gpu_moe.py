@@ -228,7 +228,8 @@ def test_quantized_swiglu(bits, M):
                                            (8, 128, 1024, "f16"), (4, 128, 512, "bf16")])
 @pytest.mark.parametrize("M", [5, 9, 16, 32, 64])
 def test_quantized_swiglu_matrix_core_pairs(bits, gs, K, xdt, M):
-    """Decode batches of 5..64 rows: gate and up row blocks alternate in one matrix-core
+    """Decode batches of 5..64 rows at 8 bits, or of one activation block (8 rows at gs 64,
+    16 at gs 128) at other widths: gate and up row blocks alternate in one matrix-core
     launch whose up item applies silu(round(g)) * round(u). Bit-equal to the grouped dense
     launch followed by the elementwise kernel (the same partial sums in the same order), with
     and without the clamp; N leaves a partial 16-row block and M a partial pass. One case is
